@@ -1,0 +1,316 @@
+"""ctypes bindings of the CPU oracle (libvtq_oracle.so).
+
+TEST INFRASTRUCTURE, NOT PRODUCT.  Only tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg import this module, always as the checker or the
+reported CPU baseline; libvtq never calls it.  See vtq_oracle.h for what each
+function restates (reference file:line on every declaration).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvtq_oracle.so")
+
+_lib = None
+
+
+class OracleError(Exception):
+    def __init__(self, code, message):
+        super().__init__(f"[{code}] {message}")
+        self.code = code
+        self.message = message
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} missing (run `make -C oracle` or __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, sz, i, f = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
+    msgp = ctypes.POINTER(ctypes.c_char_p)
+    L.vtqo_f16_to_f32.argtypes = [ctypes.c_uint16]
+    L.vtqo_f16_to_f32.restype = f
+    L.vtqo_f16_to_f32_bits.argtypes = [ctypes.c_uint16]
+    L.vtqo_f16_to_f32_bits.restype = ctypes.c_uint32
+    L.vtqo_f32_to_f16.argtypes = [f]
+    L.vtqo_f32_to_f16.restype = ctypes.c_uint16
+    L.vtqo_fixed_tree.argtypes = [vp, sz]
+    L.vtqo_fixed_tree.restype = f
+    for name in ("vtqo_canonical_chunk", "vtqo_canonical_dot", "vtqo_canonical_dot_regime2"):
+        getattr(L, name).argtypes = [vp, vp, sz]
+        getattr(L, name).restype = f
+    L.vtqo_canonical_combine.argtypes = [vp, sz]
+    L.vtqo_canonical_combine.restype = f
+    for name in ("vtqo_dequantize_q4_0", "vtqo_dequantize_q5_0", "vtqo_dequantize_q8_0", "vtqo_dequantize_q4_k",
+                 "vtqo_dequantize_q6_k"):
+        getattr(L, name).argtypes = [vp, sz, vp, msgp]
+        getattr(L, name).restype = i
+    for name in ("vtqo_quantize_q4_0", "vtqo_quantize_q8_0"):
+        getattr(L, name).argtypes = [vp, sz, vp, msgp]
+        getattr(L, name).restype = i
+    L.vtqo_quantize_block_q8.argtypes = [vp, sz, vp]
+    L.vtqo_quantize_block_q8.restype = None
+    for name in ("vtqo_dot_q4k_q8_block", "vtqo_dot_q6k_q8_block"):
+        getattr(L, name).argtypes = [vp, vp, sz]
+        getattr(L, name).restype = f
+    for name in ("vtqo_integer_dot_q4k", "vtqo_canonical_dot_q4k_fused", "vtqo_canonical_dot_q6k_fused"):
+        getattr(L, name).argtypes = [vp, vp, sz, sz, vp, msgp]
+        getattr(L, name).restype = i
+    for name in ("vtqo_linear_q4_k_integer", "vtqo_linear_q6_k_integer", "vtqo_linear_q4_k_fused",
+                 "vtqo_linear_q6_k_fused"):
+        getattr(L, name).argtypes = [vp, vp, sz, vp, sz, sz, sz, i, msgp]
+        getattr(L, name).restype = i
+    for name in ("vtqo_linear_q4_k_cpu", "vtqo_linear_q6_k_cpu", "vtqo_linear_q4_0_cpu"):
+        getattr(L, name).argtypes = [vp, sz, vp, sz, vp, sz, sz, sz, sz, msgp]
+        getattr(L, name).restype = i
+    L.vtqo_linear_dispatch.argtypes = [i, i, vp, sz, vp, sz, vp, sz, sz, sz, sz, i, msgp]
+    L.vtqo_linear_dispatch.restype = i
+    L.vtqo_matmul_f32.argtypes = [vp, vp, vp, sz, sz, sz]
+    L.vtqo_matmul_f32.restype = None
+    _lib = L
+    return L
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a
+
+
+def _u8(a):
+    if isinstance(a, (bytes, bytearray)):
+        a = np.frombuffer(a, dtype=np.uint8)
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def _check(rc, msg):
+    if rc != 0:
+        raise OracleError(rc, msg.value.decode() if msg.value else "")
+
+
+def f16_to_f32(h: int) -> np.float32:
+    return np.float32(lib().vtqo_f16_to_f32(h))
+
+
+def f16_to_f32_bits(h: int) -> int:
+    return int(lib().vtqo_f16_to_f32_bits(h))
+
+
+def f32_to_f16(v: float) -> int:
+    return int(lib().vtqo_f32_to_f16(v))
+
+
+def fixed_tree(parts) -> np.float32:
+    p = _f32(parts).copy()
+    return np.float32(lib().vtqo_fixed_tree(_ptr(p), p.size))
+
+
+def canonical_dot(x, w, n=None) -> np.float32:
+    x, w = _f32(x), _f32(w)
+    n = x.size if n is None else n
+    return np.float32(lib().vtqo_canonical_dot(_ptr(x), _ptr(w), n))
+
+
+def canonical_chunk(x, w) -> np.float32:
+    x, w = _f32(x), _f32(w)
+    return np.float32(lib().vtqo_canonical_chunk(_ptr(x), _ptr(w), x.size))
+
+
+def canonical_combine(sums) -> np.float32:
+    s = _f32(sums).copy()
+    return np.float32(lib().vtqo_canonical_combine(_ptr(s), s.size))
+
+
+def canonical_dot_regime2(x, w, n=None) -> np.float32:
+    x, w = _f32(x), _f32(w)
+    n = x.size if n is None else n
+    return np.float32(lib().vtqo_canonical_dot_regime2(_ptr(x), _ptr(w), n))
+
+
+_DEQ = {"q4_0": (32, 18), "q5_0": (32, 22), "q8_0": (32, 34), "q4_k": (256, 144), "q6_k": (256, 210)}
+
+
+def dequantize(kind: str, w) -> np.ndarray:
+    w = _u8(w)
+    numel, nbytes = _DEQ[kind]
+    out = np.zeros(max(1, (w.size // nbytes) * numel), dtype=np.float32)
+    msg = ctypes.c_char_p()
+    rc = getattr(lib(), f"vtqo_dequantize_{kind}")(_ptr(w), w.size, _ptr(out), ctypes.byref(msg))
+    _check(rc, msg)
+    return out[: (w.size // nbytes) * numel]
+
+
+def quantize(kind: str, x) -> np.ndarray:
+    x = _f32(x)
+    numel, nbytes = _DEQ[kind]
+    out = np.zeros(max(1, (x.size // numel) * nbytes), dtype=np.uint8)
+    msg = ctypes.c_char_p()
+    rc = getattr(lib(), f"vtqo_quantize_{kind}")(_ptr(x), x.size, _ptr(out), ctypes.byref(msg))
+    _check(rc, msg)
+    return out[: (x.size // numel) * nbytes]
+
+
+class Q8Block(ctypes.Structure):
+    """src/ops/quant.rs:738-743"""
+
+    _fields_ = [("d", ctypes.c_float), ("qs", ctypes.c_int8 * 256), ("bsums", ctypes.c_int32 * 8)]
+
+
+def quantize_block_q8(x) -> Q8Block:
+    x = _f32(x)
+    assert x.size <= 256
+    b = Q8Block()
+    lib().vtqo_quantize_block_q8(_ptr(x), x.size, ctypes.byref(b))
+    return b
+
+
+def dot_q4k_q8_block(w, xq: Q8Block, n=256) -> np.float32:
+    w = _u8(w)
+    return np.float32(lib().vtqo_dot_q4k_q8_block(_ptr(w), ctypes.byref(xq), n))
+
+
+def dot_q6k_q8_block(w, xq: Q8Block, n=256) -> np.float32:
+    w = _u8(w)
+    return np.float32(lib().vtqo_dot_q6k_q8_block(_ptr(w), ctypes.byref(xq), n))
+
+
+def _rowdot(name, x, w, n):
+    x, w = _f32(x), _u8(w)
+    out = ctypes.c_float()
+    msg = ctypes.c_char_p()
+    rc = getattr(lib(), name)(_ptr(x), _ptr(w), w.size, n, ctypes.byref(out), ctypes.byref(msg))
+    _check(rc, msg)
+    return np.float32(out.value)
+
+
+def integer_dot_q4k(x, w, n):
+    return _rowdot("vtqo_integer_dot_q4k", x, w, n)
+
+
+def canonical_dot_q4k_fused(x, w, n):
+    return _rowdot("vtqo_canonical_dot_q4k_fused", x, w, n)
+
+
+def canonical_dot_q6k_fused(x, w, n):
+    return _rowdot("vtqo_canonical_dot_q6k_fused", x, w, n)
+
+
+def _linear(name, x, w, batch, in_feat, out_feat, threads):
+    x, w = _f32(x), _u8(w)
+    y = np.zeros(max(1, batch * out_feat), dtype=np.float32)
+    msg = ctypes.c_char_p()
+    rc = getattr(lib(), name)(_ptr(x), _ptr(w), w.size, _ptr(y), batch, in_feat, out_feat, threads,
+                              ctypes.byref(msg))
+    _check(rc, msg)
+    return y[: batch * out_feat]
+
+
+def linear_q4_k_integer(x, w, batch, in_feat, out_feat, threads=1):
+    return _linear("vtqo_linear_q4_k_integer", x, w, batch, in_feat, out_feat, threads)
+
+
+def linear_q6_k_integer(x, w, batch, in_feat, out_feat, threads=1):
+    return _linear("vtqo_linear_q6_k_integer", x, w, batch, in_feat, out_feat, threads)
+
+
+def linear_q4_k_fused(x, w, batch, in_feat, out_feat, threads=1):
+    return _linear("vtqo_linear_q4_k_fused", x, w, batch, in_feat, out_feat, threads)
+
+
+def linear_q6_k_fused(x, w, batch, in_feat, out_feat, threads=1):
+    return _linear("vtqo_linear_q6_k_fused", x, w, batch, in_feat, out_feat, threads)
+
+
+def _linear_cpu(name, x, w, batch, in_feat, out_feat, x_len=None, y_len=None):
+    x, w = _f32(x), _u8(w)
+    y_len = batch * out_feat if y_len is None else y_len
+    y = np.zeros(max(1, y_len), dtype=np.float32)
+    msg = ctypes.c_char_p()
+    rc = getattr(lib(), name)(_ptr(x), x.size if x_len is None else x_len, _ptr(w), w.size, _ptr(y), y_len,
+                              batch, in_feat, out_feat, ctypes.byref(msg))
+    _check(rc, msg)
+    return y[:y_len]
+
+
+def linear_q4_k_cpu(x, w, batch, in_feat, out_feat):
+    return _linear_cpu("vtqo_linear_q4_k_cpu", x, w, batch, in_feat, out_feat)
+
+
+def linear_q6_k_cpu(x, w, batch, in_feat, out_feat):
+    return _linear_cpu("vtqo_linear_q6_k_cpu", x, w, batch, in_feat, out_feat)
+
+
+def linear_q4_0_cpu(x, w, batch, in_feat, out_feat, x_len=None, y_len=None):
+    return _linear_cpu("vtqo_linear_q4_0_cpu", x, w, batch, in_feat, out_feat, x_len, y_len)
+
+
+def linear_dispatch(ggml_type, regime, x, w, batch, in_feat, out_feat, threads=1):
+    x, w = _f32(x), _u8(w)
+    y = np.zeros(max(1, batch * out_feat), dtype=np.float32)
+    msg = ctypes.c_char_p()
+    rc = lib().vtqo_linear_dispatch(int(ggml_type), int(regime), _ptr(x), x.size, _ptr(w), w.size, _ptr(y),
+                                    batch * out_feat, batch, in_feat, out_feat, threads, ctypes.byref(msg))
+    _check(rc, msg)
+    return y[: batch * out_feat]
+
+
+def matmul_f32(a, b, m, k, n):
+    a, b = _f32(a), _f32(b)
+    out = np.zeros(max(1, m * n), dtype=np.float32)
+    lib().vtqo_matmul_f32(_ptr(a), _ptr(b), _ptr(out), m, k, n)
+    return out[: m * n]
+
+
+def lcg_pair(n: int):
+    """The reference's test-vector stream (src/ops/quant.rs:1856-1865): a then b from one LCG."""
+    s = 0x1234
+    mask = (1 << 64) - 1
+    vals = np.empty(2 * n, dtype=np.float32)
+    for i in range(2 * n):
+        s = (s * 6364136223846793005 + 1) & mask
+        vals[i] = np.float32(np.float32(s >> 33) / np.float32(2147483648.0)) * np.float32(2.0) - np.float32(1.0)
+    return vals[:n].copy(), vals[n:].copy()
+
+
+def _lcg_states(n: int, seed: int) -> np.ndarray:
+    """States s_1..s_n of s = s*6364136223846793005 + 1 (mod 2^64), vectorised by jumping K steps."""
+    a, mask, K = 6364136223846793005, (1 << 64) - 1, 1024
+    first = np.empty(min(n, K), dtype=np.uint64)
+    s = seed
+    for i in range(first.size):
+        s = (s * a + 1) & mask
+        first[i] = s
+    if n <= K:
+        return first
+    # s_{i+K} = A*s_i + C with A = a^K, C = sum_{t<K} a^t (mod 2^64)
+    A, C = 1, 0
+    for _ in range(K):
+        A, C = (A * a) & mask, (C * a + 1) & mask
+    out = np.empty(((n + K - 1) // K) * K, dtype=np.uint64)
+    out[:K] = first
+    with np.errstate(over="ignore"):
+        Au, Cu = np.uint64(A), np.uint64(C)
+        for j in range(1, out.size // K):
+            out[j * K:(j + 1) * K] = out[(j - 1) * K:j * K] * Au + Cu
+    return out[:n]
+
+
+def lcg_bytes(n: int, seed: int) -> np.ndarray:
+    """Byte stream of the reference's tests: s = s*6364136223846793005 + 1; byte = s >> 40
+    (src/ops/quant.rs:2018-2022)."""
+    return ((_lcg_states(n, seed) >> np.uint64(40)) & np.uint64(0xFF)).astype(np.uint8)
+
+
+def ramp_x(n: int) -> np.ndarray:
+    """Activations of the reference's tests: ((i*7919) % 1000) / 500 - 1 (src/ops/quant.rs:2023-2025)."""
+    i = np.arange(n, dtype=np.int64)
+    return (((i * 7919) % 1000).astype(np.float32) / np.float32(500.0)) - np.float32(1.0)

@@ -1,0 +1,247 @@
+"""GPU parity: libvtq (HIP, gfx950) against the pinned CPU oracle, bit for bit.
+
+Every call goes through the C ABI of include/vtq.h.  Small shapes are
+compared with the oracle run in-process; the full BASELINE configurations
+are compared with the oracle (threaded) and with the committed golden
+hashes of tests/golden/golden.json.  Non-finite outputs only need to agree
+on being NaN/Inf: IEEE-754 leaves NaN payloads unspecified and the
+reference excludes them from its own bit comparisons
+(src/ops/quant.rs:2032-2044).
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+import vtq
+from vtq import synth
+
+pytestmark = pytest.mark.gpu
+
+F = np.float32
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "golden.json")))
+THREADS = min(os.cpu_count() or 1, 16)
+
+
+def assert_bits_equal(got, want, what=""):
+    got = np.asarray(got, F).reshape(-1)
+    want = np.asarray(want, F).reshape(-1)
+    assert got.shape == want.shape, what
+    fin = np.isfinite(want)
+    bad = np.nonzero(got[fin].view(np.uint32) != want[fin].view(np.uint32))[0]
+    assert bad.size == 0, (
+        f"{what}: {bad.size} of {fin.sum()} finite outputs differ; first at {np.nonzero(fin)[0][bad[0]]}: "
+        f"gpu {got[fin][bad[0]]!r} ({got[fin].view(np.uint32)[bad[0]]:08x}) vs "
+        f"oracle {want[fin][bad[0]]!r} ({want[fin].view(np.uint32)[bad[0]]:08x})")
+    assert np.array_equal(np.isnan(got[~fin]), np.isnan(want[~fin])), what
+    assert np.array_equal(got[~fin & ~np.isnan(want)], want[~fin & ~np.isnan(want)]), what
+
+
+def run_gpu(ctx, ggml_type, regime, x, w, batch, in_f, out_f):
+    y = np.full(batch * out_f, np.nan, F)
+    print(f"[gpu] type={vtq.TYPE_NAMES.get(ggml_type, ggml_type)} regime={regime} batch={batch} "
+          f"in={in_f} out={out_f}", flush=True)
+    ctx.linear(ggml_type, regime, x, w, y, batch, in_f, out_f)
+    return y
+
+
+def pinned_q4k(rows, in_f, seed):
+    w = O.lcg_bytes(rows * (in_f // 256) * 144, seed).reshape(-1, 144)
+    w[:, 0:2] = np.frombuffer(np.uint16(0x2E66).tobytes(), np.uint8)
+    w[:, 2:4] = np.frombuffer(np.uint16(0x2666).tobytes(), np.uint8)
+    return w.reshape(-1)
+
+
+def pinned_q6k(rows, in_f, seed):
+    w = O.lcg_bytes(rows * (in_f // 256) * 210, seed).reshape(-1, 210)
+    w[:, 208:210] = np.frombuffer(np.uint16(0x2E66).tobytes(), np.uint8)
+    return w.reshape(-1)
+
+
+def check(ctx, ggml_type, regime, x, w, batch, in_f, out_f):
+    got = run_gpu(ctx, ggml_type, regime, x, w, batch, in_f, out_f)
+    want = O.linear_dispatch(ggml_type, regime, x, w, batch, in_f, out_f, THREADS)
+    assert_bits_equal(got, want, f"type {ggml_type} regime {regime} {batch}x{in_f}->{out_f}")
+    return got
+
+
+# ------------------------------------------------------------ k-quant integer
+
+KQ_SHAPES = [(1, 256, 1), (1, 256, 3), (1, 512, 7), (1, 4096, 64), (1, 11008, 17), (3, 4096, 300),
+             (1, 2048, 2048), (1, 2048, 256), (1, 5632, 2048), (2, 4096 * 4 + 256, 33), (1, 65536, 9)]
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", KQ_SHAPES)
+def test_q4k_integer_synthetic(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 7 + out_f)
+    x = synth.activations(batch * in_f, seed=in_f + batch)
+    check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", KQ_SHAPES)
+def test_q6k_integer_synthetic(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.Q6_K, out_f, in_f, seed=in_f * 11 + out_f)
+    x = synth.activations(batch * in_f, seed=in_f + 3 * batch)
+    check(ctx, vtq.Q6_K, 0, x, w, batch, in_f, out_f)
+
+
+@pytest.mark.parametrize("in_f,out_f", [(256, 3), (1024, 7), (4096, 31), (14336, 5)])
+def test_kquant_random_bytes(ctx, in_f, out_f):
+    # the reference's LCG byte blocks with pinned finite scales, ramp activations
+    x = O.ramp_x(in_f)
+    check(ctx, vtq.Q4_K, 0, x, pinned_q4k(out_f, in_f, 0xC0FFEE), 1, in_f, out_f)
+    check(ctx, vtq.Q6_K, 0, x, pinned_q6k(out_f, in_f, 0xBEEF), 1, in_f, out_f)
+
+
+def test_kquant_unrestricted_bytes(ctx):
+    # arbitrary bytes: f16 scales may be Inf/NaN/subnormal; finite outputs must match
+    in_f, out_f = 2048, 64
+    x = synth.activations(in_f, seed=99)
+    check(ctx, vtq.Q4_K, 0, x, synth.random_bytes(out_f * 8 * 144, 5), 1, in_f, out_f)
+    check(ctx, vtq.Q6_K, 0, x, synth.random_bytes(out_f * 8 * 210, 6), 1, in_f, out_f)
+
+
+def test_activation_edge_cases(ctx):
+    # zero blocks, NaN, +-Inf, subnormals, huge values, exact ties, -0.0
+    in_f, out_f = 8 * 256, 40
+    x = synth.activations(in_f, seed=3)
+    x[0:256] = 0.0
+    x[256:512] = -0.0
+    x[512] = np.nan
+    x[800] = np.inf
+    x[1024:1280] = (x[1024:1280] * F(1e-42)).astype(F)  # subnormal block
+    x[1280:1536] = (x[1280:1536] * F(3e37)).astype(F)
+    x[1536] = 127.0
+    x[1537] = F(0.5) - F(2.0 ** -25)
+    x[1538:1600] = np.arange(62, dtype=F) + F(0.5)
+    for t in (vtq.Q4_K, vtq.Q6_K):
+        w = synth.weights(t, out_f, in_f, seed=t)
+        check(ctx, t, 0, x, w, 1, in_f, out_f)
+
+
+# ------------------------------------------------------------- canonical dot
+
+CANON_SHAPES = [(1, 32, 1), (1, 64, 5), (1, 4096, 33), (2, 4096, 100), (1, 8192, 9), (1, 8192 + 32, 9),
+                (1, 14336, 17), (1, 11008, 40), (1, 65536, 3), (3, 2048, 70)]
+
+
+@pytest.mark.parametrize("ggml_type", [vtq.Q8_0, vtq.Q5_0, vtq.Q4_0])
+@pytest.mark.parametrize("batch,in_f,out_f", CANON_SHAPES)
+def test_canonical_block_formats(ctx, ggml_type, batch, in_f, out_f):
+    w = synth.weights(ggml_type, out_f, in_f, seed=in_f * 13 + out_f + ggml_type)
+    x = synth.activations(batch * in_f, seed=in_f * 5 + batch)
+    check(ctx, ggml_type, 0, x, w, batch, in_f, out_f)
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", CANON_SHAPES[:8] + [(1, 13, 4), (1, 4100, 7), (2, 8195, 5)])
+def test_canonical_f32(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.F32, out_f, in_f, seed=in_f * 17 + out_f, sigma=1.0)
+    x = synth.activations(batch * in_f, seed=in_f * 19 + batch)
+    check(ctx, vtq.F32, 0, x, w, batch, in_f, out_f)
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", [(1, 256, 3), (1, 4096, 50), (1, 8192, 3), (1, 14336, 9),
+                                              (2, 11008, 20), (1, 65536, 2)])
+def test_q4k_float_fused_regime(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 23 + out_f)
+    x = synth.activations(batch * in_f, seed=in_f * 29 + batch)
+    check(ctx, vtq.Q4_K, 1, x, w, batch, in_f, out_f)
+
+
+def test_canonical_reference_vectors(ctx):
+    # F32 arm on the reference's LCG pair: must land on the pinned bits.
+    for n, want in ((4096, 0x40CE39E1), (14336, 0xC1A3BF11)):
+        a, b = O.lcg_pair(n)
+        y = run_gpu(ctx, vtq.F32, 0, a, b.view(np.uint8), 1, n, 1)
+        assert int(y.view(np.uint32)[0]) == want
+
+
+# -------------------------------------------------------- full configurations
+
+
+@pytest.mark.parametrize("name", ["q8_0_4096x4096", "q4k_11008x4096", "q4k_4096x11008", "q6k_32000x4096"])
+def test_full_config_bit_exact(ctx, name):
+    cfg = synth.CONFIGS[name]
+    g = GOLDEN["configs"][name]
+    x, w = cfg.make()
+    assert hashlib.sha256(w.tobytes()).hexdigest() == g["w_sha256"], "generator drift (weights)"
+    assert hashlib.sha256(x.tobytes()).hexdigest() == g["x_sha256"], "generator drift (activations)"
+    got = run_gpu(ctx, cfg.ggml_type, 0, x, w, cfg.batch, cfg.in_feat, cfg.out_feat)
+    want = O.linear_dispatch(cfg.ggml_type, 0, x, w, cfg.batch, cfg.in_feat, cfg.out_feat, THREADS)
+    assert_bits_equal(got, want, name)
+    assert hashlib.sha256(got.tobytes()).hexdigest() == g["y_sha256"]
+
+
+def test_determinism_repeat_calls(ctx):
+    cfg = synth.CONFIGS["q4k_4096x11008"]
+    x, w = cfg.make()
+    a = run_gpu(ctx, cfg.ggml_type, 0, x, w, 1, cfg.in_feat, cfg.out_feat)
+    for _ in range(3):
+        b = run_gpu(ctx, cfg.ggml_type, 0, x, w, 1, cfg.in_feat, cfg.out_feat)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ------------------------------------------------------- edges and errors
+
+
+def test_empty_and_degenerate_shapes(ctx):
+    y = np.full(3, np.nan, F)
+    ctx.linear(vtq.Q4_K, 0, np.zeros(0, F), np.zeros(0, np.uint8), y, 1, 0, 3)
+    assert y.tolist() == [0.0, 0.0, 0.0] and not np.signbit(y).any()
+    y = np.full(4, 7.0, F)
+    ctx.linear(vtq.Q6_K, 0, np.zeros(0, F), np.zeros(0, np.uint8), y, 0, 256, 4)
+    assert y.tolist() == [7.0] * 4  # batch 0 writes nothing
+    ctx.linear(vtq.Q8_0, 0, np.zeros(64, F), np.zeros(0, np.uint8), np.zeros(1, F), 1, 64, 0)
+
+
+def test_errors_mirror_reference(ctx):
+    y = np.zeros(4, F)
+    with pytest.raises(vtq.Internal, match="linear_q4_k_integer: in_feat not a multiple of 256"):
+        ctx.linear_q4_k_integer(np.zeros(100, F), np.zeros(144, np.uint8), y, 1, 100, 1)
+    with pytest.raises(vtq.Internal, match="linear_q4_k_integer: weight shape mismatch"):
+        ctx.linear_q4_k_integer(np.zeros(256, F), np.zeros(143, np.uint8), y, 1, 256, 1)
+    with pytest.raises(vtq.Internal, match="linear_q6_k_integer_parallel: weight shape"):
+        ctx.linear(vtq.Q6_K, 0, np.zeros(256, F), np.zeros(100, np.uint8), np.zeros(600, F), 1, 256, 600)
+    with pytest.raises(vtq.NotImplementedDtype, match="weight dtype not"):
+        ctx.linear(vtq.F16, 0, np.zeros(32, F), np.zeros(64, np.uint8), y, 1, 32, 1)
+    with pytest.raises(vtq.Internal, match="linear_q4_0: x size mismatch"):
+        ctx.linear_q4_0(np.zeros(31, F), np.zeros(18, np.uint8), np.zeros(1, F), 1, 32, 1)
+    with pytest.raises(vtq.Internal, match="x shorter"):
+        ctx.linear_q4_k_integer(np.zeros(255, F), np.zeros(144, np.uint8), y, 1, 256, 1)
+    with pytest.raises(vtq.NotImplementedDtype):
+        ctx.linear(vtq.Q4_K, 0, np.zeros(65536 + 256, F), np.zeros((65536 + 256) // 256 * 144, np.uint8),
+                   np.zeros(1, F), 1, 65536 + 256, 1)
+    # the context stays usable after errors
+    test_q4k_integer_synthetic(ctx, 1, 256, 3)
+
+
+def test_weight_cache_rekeys_on_length_and_release(ctx):
+    in_f, out_f = 512, 8
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=1)
+    x = synth.activations(in_f, seed=2)
+    a = run_gpu(ctx, vtq.Q4_K, 0, x, w, 1, in_f, out_f)
+    w2 = w.copy()
+    w2[:] = synth.weights(vtq.Q4_K, out_f, in_f, seed=3)
+    ctx.release_weights(w2)
+    b = run_gpu(ctx, vtq.Q4_K, 0, x, w2, 1, in_f, out_f)
+    assert_bits_equal(b, O.linear_dispatch(vtq.Q4_K, 0, x, w2, 1, in_f, out_f), "w2")
+    ctx.release_weights()
+    assert_bits_equal(run_gpu(ctx, vtq.Q4_K, 0, x, w, 1, in_f, out_f), a, "after release")
+
+
+def test_device_pointer_entry_matches_host(ctx):
+    import torch
+
+    cfg = synth.CONFIGS["q4k_11008x4096"]
+    x, w = cfg.make(rows=1000)
+    dx = torch.from_numpy(x).cuda()
+    dw = torch.from_numpy(w).cuda()
+    dy = torch.full((1000,), float("nan"), device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    ctx.linear_device(vtq.Q4_K, 0, dx.data_ptr(), dw.data_ptr(), w.size, dy.data_ptr(), 1, cfg.in_feat, 1000, stream)
+    torch.cuda.synchronize()
+    want = O.linear_dispatch(vtq.Q4_K, 0, x, w, 1, cfg.in_feat, 1000, THREADS)
+    assert_bits_equal(dy.cpu().numpy(), want, "device entry")

@@ -1,0 +1,131 @@
+// vtq_device.h -- gfx950 device primitives shared by the vtq kernels.
+//
+// Everything here is exact or is a single IEEE binary32 operation in source
+// order: the library is compiled with -ffp-contract=off, fp32 division is
+// the correctly rounded v_div_scale/v_div_fmas/v_div_fixup sequence, and the
+// kernel descriptors keep fp32/fp16 denormals (float_denorm_mode 3).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vtq {
+
+constexpr int kWave = 64;
+
+// A 16-byte vector that only promises 4-byte alignment, so that the
+// compiler may still emit one global_load_dwordx4 for it.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+// IEEE binary16 bits -> binary32, exact, NaN payload kept unquieted
+// (src/ops/quant.rs:40-66).  A subnormal half m*2^-24 is formed by an exact
+// float product.
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu;
+    const uint32_t m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0u) {
+        bits = __float_as_uint((float)m * 0x1p-24f) | sign;
+    } else if (e == 0x1Fu) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+// Rust `(t as i32).clamp(-127, 127)` for the activation quantizer: NaN -> 0,
+// truncation toward zero, saturation (src/ops/quant.rs:766).
+__device__ __forceinline__ int quant_round_clamp(float t) {
+    if (t != t) return 0;
+    if (t >= 127.0f) return 127;
+    if (t <= -127.0f) return -127;
+    return (int)t;  // |t| < 127: exact truncation
+}
+
+// q = clamp(trunc(x*inv + (x*inv >= 0 ? 0.5 : -0.5)))  (src/ops/quant.rs:764-766)
+__device__ __forceinline__ int quant_one(float v, float inv) {
+    const float s = v * inv;
+    const float t = s + (s >= 0.0f ? 0.5f : -0.5f);
+    return quant_round_clamp(t);
+}
+
+// |v| exactly as the reference forms it: (v < 0) ? -v : v (so -0.0 stays -0.0).
+__device__ __forceinline__ float abs_ref(float v) { return v < 0.0f ? -v : v; }
+
+// max in the reference's sense: keep m unless a > m (NaN never wins).
+__device__ __forceinline__ float max_ref(float m, float a) { return a > m ? a : m; }
+
+// ---- cross-lane helpers (DPP within quads/rows, bpermute across rows) ----
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;
+
+// Sum over the 4 lanes of a quad (integer: any order is exact).
+__device__ __forceinline__ int quad_sum_i(int v) {
+    v += dpp_i<kQuadXor1>(v);
+    v += dpp_i<kQuadXor2>(v);
+    return v;
+}
+
+__device__ __forceinline__ float shfl_down_f(float v, int delta) {
+    return __shfl_down(v, delta, kWave);
+}
+__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
+
+// Wave-wide maximum in the reference's sense.
+__device__ __forceinline__ float wave_max_ref(float m) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max_ref(m, shfl_xor_f(m, off));
+    return m;
+}
+
+// Quantize one 256-element activation block with one wave: lane L holds
+// elements 4L..4L+3 in v.  Produces (src/ops/quant.rs:750-771):
+//   *packed : the lane's four int8 codes, element 4L in the low byte
+//   *s16    : sum of the 16-element run containing the lane (lanes 4r..4r+3)
+//   *s32    : sum of the 32-element sub-block containing the lane (bsums)
+//   return  : d = amax / 127
+__device__ __forceinline__ float quant_block_wave(float4 v, uint32_t* packed, int* s16, int* s32) {
+    float m = 0.0f;
+    m = max_ref(m, abs_ref(v.x));
+    m = max_ref(m, abs_ref(v.y));
+    m = max_ref(m, abs_ref(v.z));
+    m = max_ref(m, abs_ref(v.w));
+    const float amax = wave_max_ref(m);
+    const float d = amax / 127.0f;
+    const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+    const int q0 = quant_one(v.x, inv), q1 = quant_one(v.y, inv);
+    const int q2 = quant_one(v.z, inv), q3 = quant_one(v.w, inv);
+    *packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+              ((uint32_t)(q3 & 0xFF) << 24);
+    int s = q0 + q1 + q2 + q3;
+    s = quad_sum_i(s);  // 16-element run
+    *s16 = s;
+    s += dpp_i<kRowHalfMirror>(s);  // lanes i and 7-i of each 8-lane group
+    *s32 = s;
+    return d;
+}
+
+// fixed_tree (src/ops/quant.rs:461-476) over values held in lane groups:
+// group g of width W lanes (the value replicated or at least held in the
+// group's first lane), G groups, n valid groups; slots >= n must hold -0.0f
+// (x + -0.0 == x for every x, so padded slots never change a sum).
+// Pairing at stride s: slot i (multiple of 2s) += slot i+s.  This equals the
+// reference's level-by-level halving: level k pairs the 2^k-blocks starting
+// at multiples of 2^(k+1), and an unpaired trailing block passes through.
+// The result is in the first lane of group 0 (lane 0).
+template <int W, int G>
+__device__ __forceinline__ float group_tree(float v) {
+#pragma unroll
+    for (int s = 1; s < G; s <<= 1) v += shfl_down_f(v, s * W);
+    return v;
+}
+
+}  // namespace vtq

@@ -1,0 +1,38 @@
+/*
+ * vtq_synth.h -- seeded synthetic GGUF blocks and activations for the
+ * benchmark configurations (not part of the C ABI; used by tests and
+ * bench.py on both sides of a parity check).
+ *
+ * Stream: SplitMix64.  Uniform integers in [0, range): (u >> 32) % range.
+ * Gaussian: Box-Muller in double (cos branch only), cast to float.
+ * fp16 scales: IEEE round-to-nearest-even encode, subnormals kept.
+ *
+ * Per block, draws are taken in this order:
+ *   Q4_K: d, dmin, sc[0..8], m[0..8], nibble[0..256] (element order)
+ *   Q6_K: d, sc[0..16] (U[-64,63]), code[0..256] (U[0,63], element order)
+ *   Q8_0: d, code[0..32] (U[-127,127])
+ *   Q5_0: d, code[0..32] (U[0,31], element order)
+ *   Q4_0: d, code[0..32] (U[0,15], element order)
+ * with d, dmin = f16(|N(0, sigma)|).
+ */
+#ifndef VTQ_SYNTH_H
+#define VTQ_SYNTH_H
+#include <stddef.h>
+#include <stdint.h>
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+uint16_t vtqs_f32_to_f16_rne(float f);
+void vtqs_normal_f32(uint64_t seed, float *out, size_t n, float sigma);
+void vtqs_q4_k(uint64_t seed, uint8_t *w, size_t rows, size_t in_feat, float sigma);
+void vtqs_q6_k(uint64_t seed, uint8_t *w, size_t rows, size_t in_feat, float sigma);
+void vtqs_q8_0(uint64_t seed, uint8_t *w, size_t rows, size_t in_feat, float sigma);
+void vtqs_q5_0(uint64_t seed, uint8_t *w, size_t rows, size_t in_feat, float sigma);
+void vtqs_q4_0(uint64_t seed, uint8_t *w, size_t rows, size_t in_feat, float sigma);
+void vtqs_bytes(uint64_t seed, uint8_t *w, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

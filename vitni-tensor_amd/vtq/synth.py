@@ -1,0 +1,114 @@
+"""Seeded synthetic workloads of the benchmark configurations.
+
+Wraps libvtq_synth.so (generator specified in synth/vtq_synth.h).  The same
+bytes are produced on every machine with this image, so tests and the
+benchmark feed the GPU path and the CPU oracle identical inputs.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import BLOCK, F32, LIB_DIR, Q4_0, Q4_K, Q5_0, Q6_K, Q8_0
+
+SEED_BASE = 0x5654_5100_0000_0000
+X_SEED_OFFSET = 0x80
+SCALE_SIGMA = 0.01  # d, dmin = f16(|N(0, 0.01)|)
+
+_synth = None
+
+
+def lib() -> ctypes.CDLL:
+    global _synth
+    if _synth is None:
+        path = os.path.join(LIB_DIR, "libvtq_synth.so")
+        if not os.path.exists(path):
+            raise ImportError(f"{path} is missing (run __graft_entry__.build())")
+        s = ctypes.CDLL(path)
+        u64, vp, sz, f = ctypes.c_uint64, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float
+        for name in ("vtqs_q4_k", "vtqs_q6_k", "vtqs_q8_0", "vtqs_q5_0", "vtqs_q4_0"):
+            getattr(s, name).argtypes = [u64, vp, sz, sz, f]
+            getattr(s, name).restype = None
+        s.vtqs_normal_f32.argtypes = [u64, vp, sz, f]
+        s.vtqs_normal_f32.restype = None
+        s.vtqs_bytes.argtypes = [u64, vp, sz]
+        s.vtqs_bytes.restype = None
+        s.vtqs_f32_to_f16_rne.argtypes = [f]
+        s.vtqs_f32_to_f16_rne.restype = ctypes.c_uint16
+        _synth = s
+    return _synth
+
+
+def weights(ggml_type: int, rows: int, in_feat: int, seed: int, sigma: float = SCALE_SIGMA) -> np.ndarray:
+    """GGUF blocks of W[rows, in_feat] (uint8), generator of vtq_synth.h."""
+    s = lib()
+    if ggml_type == F32:
+        w = np.empty(rows * in_feat, dtype=np.float32)
+        s.vtqs_normal_f32(seed, w.ctypes.data, w.size, sigma)
+        return w.view(np.uint8)
+    numel, nbytes = BLOCK[ggml_type]
+    assert in_feat % numel == 0
+    w = np.empty(rows * (in_feat // numel) * nbytes, dtype=np.uint8)
+    fn = {Q4_K: s.vtqs_q4_k, Q6_K: s.vtqs_q6_k, Q8_0: s.vtqs_q8_0, Q5_0: s.vtqs_q5_0, Q4_0: s.vtqs_q4_0}[ggml_type]
+    fn(seed, w.ctypes.data, rows, in_feat, sigma)
+    return w
+
+
+def activations(n: int, seed: int, sigma: float = 1.0) -> np.ndarray:
+    x = np.empty(n, dtype=np.float32)
+    lib().vtqs_normal_f32(seed, x.ctypes.data, n, sigma)
+    return x
+
+
+def random_bytes(n: int, seed: int) -> np.ndarray:
+    w = np.empty(n, dtype=np.uint8)
+    lib().vtqs_bytes(seed, w.ctypes.data, n)
+    return w
+
+
+@dataclass(frozen=True)
+class Config:
+    """One BASELINE.json configuration of the linear layer."""
+
+    index: int
+    name: str
+    ggml_type: int
+    out_feat: int
+    in_feat: int
+    batch: int
+
+    @property
+    def w_seed(self) -> int:
+        return SEED_BASE + self.index
+
+    @property
+    def x_seed(self) -> int:
+        return SEED_BASE + self.index + X_SEED_OFFSET
+
+    def make(self, rows: int | None = None, batch: int | None = None):
+        """(x, w) for the first `rows` output rows (default all) and `batch` rows of x."""
+        rows = self.out_feat if rows is None else rows
+        batch = self.batch if batch is None else batch
+        w = weights(self.ggml_type, rows, self.in_feat, self.w_seed)
+        x = activations(batch * self.in_feat, self.x_seed)
+        return x, w
+
+    def weight_bytes(self) -> int:
+        numel, nbytes = BLOCK[self.ggml_type]
+        return self.out_feat * (self.in_feat // numel) * nbytes
+
+    def algorithmic_bytes(self) -> int:
+        """Packed weights + fp32 activations in + fp32 outputs out."""
+        return self.weight_bytes() + 4 * self.batch * (self.in_feat + self.out_feat)
+
+
+CONFIGS = {
+    "q8_0_4096x4096": Config(0, "q8_0_4096x4096", Q8_0, 4096, 4096, 1),
+    "q4k_11008x4096": Config(1, "q4k_11008x4096", Q4_K, 11008, 4096, 1),
+    "q4k_4096x11008": Config(2, "q4k_4096x11008", Q4_K, 4096, 11008, 1),
+    "q6k_32000x4096": Config(3, "q6k_32000x4096", Q6_K, 32000, 4096, 1),
+    "q4k_gemm_14336x4096_m512": Config(4, "q4k_gemm_14336x4096_m512", Q4_K, 14336, 4096, 512),
+}
