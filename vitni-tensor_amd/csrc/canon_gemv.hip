@@ -111,7 +111,8 @@ __global__ __launch_bounds__(256) void canon_gemv_kernel(const float* __restrict
                                                           int nchunks) {
     constexpr int kRowsPerWave = 8 / CPW;
     constexpr int P = Dec::kBlock / 8;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
     const int j = lane & 7, u = lane >> 3;
     const int c = u % CPW;
     const int o = (blockIdx.x * 4 + wave) * kRowsPerWave + u / CPW;

@@ -120,7 +120,7 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
                 return set_err(c, VTQ_E_INTERNAL, serial_names ? "linear_q4_k_integer: weight shape mismatch"
                                                                : "linear_q4_k_integer_parallel: weight shape");
             if (in_feat > (size_t)vtq::kquant_max_in_feat())
-                return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 65536 for k-quant GEMV");
+                return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 32768 for k-quant GEMV");
             p->kind = Plan::kQ4KInt;
         } else {
             return set_err(c, VTQ_E_INVALID_ARGUMENT, "vtq: unknown regime");
@@ -135,7 +135,7 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
             return set_err(c, VTQ_E_INTERNAL, serial_names ? "linear_q6_k_integer: weight shape mismatch"
                                                            : "linear_q6_k_integer_parallel: weight shape");
         if (in_feat > (size_t)vtq::kquant_max_in_feat())
-            return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 65536 for k-quant GEMV");
+            return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 32768 for k-quant GEMV");
         p->kind = Plan::kQ6KInt;
         break;
     case VTQ_TYPE_Q8_0:

@@ -13,6 +13,11 @@ namespace vtq {
 
 constexpr int kWave = 64;
 
+// Index of the calling wave in its workgroup, as a uniform (scalar) value:
+// without readfirstlane the compiler treats threadIdx.x >> 6 as divergent and
+// turns every loop over a wave's work into an exec-masked vector loop.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // A 16-byte vector that only promises 4-byte alignment, so that the
 // compiler may still emit one global_load_dwordx4 for it.
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -35,19 +40,29 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
     return __uint_as_float(bits);
 }
 
-// Rust `(t as i32).clamp(-127, 127)` for the activation quantizer: NaN -> 0,
-// truncation toward zero, saturation (src/ops/quant.rs:766).
-__device__ __forceinline__ int quant_round_clamp(float t) {
-    if (t != t) return 0;
-    if (t >= 127.0f) return 127;
-    if (t <= -127.0f) return -127;
-    return (int)t;  // |t| < 127: exact truncation
+// The same conversion with v_cvt_f32_f16: exact for every finite value and
+// +-Inf (fp16 denormals are preserved by the kernel's float mode); a NaN
+// comes out quieted, which only changes NaN payloads.
+__device__ __forceinline__ float f16_hw(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
-// q = clamp(trunc(x*inv + (x*inv >= 0 ? 0.5 : -0.5)))  (src/ops/quant.rs:764-766)
+// Rust `(t as i32).clamp(-127, 127)` for the activation quantizer: NaN -> 0,
+// truncation toward zero, saturation (src/ops/quant.rs:766).  Branch-free:
+// clamp in float (exact), truncate (exact for |c| <= 127), and select 0
+// for an unordered t.
+__device__ __forceinline__ int quant_round_clamp(float t) {
+    const float c = fminf(fmaxf(t, -127.0f), 127.0f);
+    const int q = (int)c;
+    return (t == t) ? q : 0;
+}
+
+// q = clamp(trunc(s + (s >= 0 ? 0.5 : -0.5))), s = x*inv (src/ops/quant.rs:764-766).
+// copysign(0.5, s) differs from the reference's bias only at s = -0.0, where
+// both -0.0 + 0.5 and -0.0 - 0.5 truncate to 0, so q is the same for every s.
 __device__ __forceinline__ int quant_one(float v, float inv) {
     const float s = v * inv;
-    const float t = s + (s >= 0.0f ? 0.5f : -0.5f);
+    const float t = s + copysignf(0.5f, s);
     return quant_round_clamp(t);
 }
 
@@ -65,7 +80,8 @@ __device__ __forceinline__ int dpp_i(int v) {
 }
 constexpr int kQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
 constexpr int kQuadXor2 = 0x4E;     // quad_perm [2,3,0,1]
-constexpr int kRowHalfMirror = 0x141;
+constexpr int kRowHalfMirror = 0x141;  // lane i <-> 7-i within 8
+constexpr int kRowMirror = 0x140;      // lane i <-> 15-i within 16
 
 // Sum over the 4 lanes of a quad (integer: any order is exact).
 __device__ __forceinline__ int quad_sum_i(int v) {
@@ -79,11 +95,19 @@ __device__ __forceinline__ float shfl_down_f(float v, int delta) {
 }
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, kWave); }
 
-// Wave-wide maximum in the reference's sense.
-__device__ __forceinline__ float wave_max_ref(float m) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = max_ref(m, shfl_xor_f(m, off));
-    return m;
+// Wave-wide maximum of per-lane values that are all non-NaN and >= +0.0
+// (each lane's value came from max_ref starting at +0.0), so v_max_f32 is
+// exact and order-free.  DPP inside each 16-lane row, readlane across rows.
+__device__ __forceinline__ float wave_max_nonneg(float m) {
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), kQuadXor1, 0xF, 0xF, true)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), kQuadXor2, 0xF, 0xF, true)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), kRowHalfMirror, 0xF, 0xF, true)));
+    m = fmaxf(m, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(m), kRowMirror, 0xF, 0xF, true)));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(m), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
 // Quantize one 256-element activation block with one wave: lane L holds
@@ -98,7 +122,7 @@ __device__ __forceinline__ float quant_block_wave(float4 v, uint32_t* packed, in
     m = max_ref(m, abs_ref(v.y));
     m = max_ref(m, abs_ref(v.z));
     m = max_ref(m, abs_ref(v.w));
-    const float amax = wave_max_ref(m);
+    const float amax = wave_max_nonneg(m);
     const float d = amax / 127.0f;
     const float inv = d != 0.0f ? 1.0f / d : 0.0f;
     const int q0 = quant_one(v.x, inv), q1 = quant_one(v.y, inv);

@@ -79,6 +79,15 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         return _lib
     if not os.path.exists(path):
         raise ImportError(f"libvtq.so not built: {path} is missing (run __graft_entry__.build())")
+    # One HIP runtime per process: torch's ROCm wheel loads its own
+    # libamdhip64 (NEEDED "libamdhip64.so", SONAME libamdhip64.so.7).  Loading
+    # torch first lets libvtq's NEEDED libamdhip64.so.7 resolve to that same
+    # copy by SONAME; the other order would map a second runtime into the
+    # process and the second one would find no device.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
     lib.vtq_create.argtypes = [i, ctypes.POINTER(vp)]
@@ -112,7 +121,13 @@ EXPORTED = (
 
 
 class Context:
-    """One libvtq context (one HIP device, used by one thread at a time)."""
+    """One libvtq context (one HIP device, used by one thread at a time).
+
+    Host-pointer calls cache the weight bytes on the device keyed by the
+    array's address and length, as the reference's weights are immutable
+    views into a GGUF blob.  Call release_weights() before reusing or freeing
+    a weight array whose bytes change.
+    """
 
     def __init__(self, device: int = 0):
         self.lib = load_library()
