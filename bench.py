@@ -41,7 +41,8 @@ WORKLOADS = {
     "q6k_gemv_lm_head": ["q6k_32000x4096"],
     "q4k_gemm_prefill": ["q4k_gemm_14336x4096_m512"],
 }
-KERNEL_NAME = {12: "q4k_gemv_kernel", 14: "q6k_gemv_kernel", 8: "canon_gemv_kernel<DecQ8_0>"}
+KERNEL_NAME = {12: "kquant_gemv_kernel<Q4K>", 14: "kquant_gemv_kernel<Q6K>", 8: "canon_gemv_kernel<DecQ8_0>"}
+INT8_MFMA_PEAK_TOPS = 5000.0
 
 
 def parse():
@@ -173,6 +174,8 @@ def main():
     mean_launch_us = statistics.mean(launch_us)
     per_launch_bytes = step_bytes / len(cfgs)
     achieved = per_launch_bytes / (mean_launch_us * 1e-6) / 1e9
+    gemm = cfgs[0].batch >= 32
+    step_ops = sum(2 * c.batch * c.out_feat * c.in_feat for c in cfgs)
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
@@ -203,12 +206,13 @@ def main():
             "bit_exact_vs_oracle": bit_exact,
         },
         "roofline": {
-            "bound": "hbm",
-            "kernel": KERNEL_NAME.get(cfgs[0].ggml_type, "?"),
-            "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "bound": "mfma" if gemm else "hbm",
+            "kernel": "q4k_gemm_kernel (+ act_quant_rows_kernel)" if gemm else KERNEL_NAME.get(cfgs[0].ggml_type, "?"),
+            "achieved": round(step_ops / len(cfgs) / (mean_launch_us * 1e-6) / 1e12, 2) if gemm else round(achieved, 2),
+            "peak": INT8_MFMA_PEAK_TOPS if gemm else HBM_PEAK_GBS,
+            "unit": "TOPS" if gemm else "GB/s",
+            "frac": round(step_ops / len(cfgs) / (mean_launch_us * 1e-6) / 1e12 / INT8_MFMA_PEAK_TOPS, 4) if gemm
+            else round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "launch_us_mean": [round(v, 3) for v in launch_us],
             "launch_us_median": [round(v, 3) for v in launch_med_us],

@@ -92,6 +92,33 @@ def test_q6k_integer_synthetic(ctx, batch, in_f, out_f):
     check(ctx, vtq.Q6_K, 0, x, w, batch, in_f, out_f)
 
 
+# batch >= 32 takes the i8-MFMA prefill GEMM (token tiles of 128, row tiles of 32)
+GEMM_SHAPES = [(32, 256, 32), (33, 512, 1), (64, 4096, 100), (130, 2048, 70), (128, 5632, 64),
+               (256, 11008, 40), (40, 256 * 127, 8), (300, 4096, 33)]
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", GEMM_SHAPES)
+def test_q4k_prefill_gemm(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 31 + out_f)
+    x = synth.activations(batch * in_f, seed=in_f * 37 + batch)
+    check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
+
+
+def test_q4k_prefill_gemm_edge_activations(ctx):
+    batch, in_f, out_f = 48, 1024, 40
+    x = synth.activations(batch * in_f, seed=5).reshape(batch, in_f)
+    x[0] = 0.0                     # an all-zero token
+    x[1] = -0.0
+    x[2, :256] = np.nan
+    x[3, 7] = np.inf
+    x[4] = (x[4] * F(1e-42)).astype(F)
+    x[5] = (x[5] * F(3e37)).astype(F)
+    x[6, :64] = np.arange(64, dtype=F) + F(0.5)
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=77)
+    check(ctx, vtq.Q4_K, 0, x.reshape(-1), w, batch, in_f, out_f)
+    check(ctx, vtq.Q4_K, 0, x.reshape(-1), pinned_q4k(out_f, in_f, 0xC0FFEE), batch, in_f, out_f)
+
+
 @pytest.mark.parametrize("in_f,out_f", [(256, 3), (1024, 7), (4096, 31), (14336, 5)])
 def test_kquant_random_bytes(ctx, in_f, out_f):
     # the reference's LCG byte blocks with pinned finite scales, ramp activations
@@ -166,7 +193,8 @@ def test_canonical_reference_vectors(ctx):
 # -------------------------------------------------------- full configurations
 
 
-@pytest.mark.parametrize("name", ["q8_0_4096x4096", "q4k_11008x4096", "q4k_4096x11008", "q6k_32000x4096"])
+@pytest.mark.parametrize("name", ["q8_0_4096x4096", "q4k_11008x4096", "q4k_4096x11008", "q6k_32000x4096",
+                                  "q4k_gemm_14336x4096_m512"])
 def test_full_config_bit_exact(ctx, name):
     cfg = synth.CONFIGS[name]
     g = GOLDEN["configs"][name]

@@ -35,6 +35,7 @@ struct vtq_ctx {
     int num_cus = 0;
     hipStream_t stream = nullptr;
     DevBuf dx, dy;          // device staging for the host-pointer path
+    DevBuf ws;              // kernel workspace (quantized activations of the GEMM path)
     void* hx = nullptr;     // pinned staging
     size_t hx_cap = 0;
     void* hy = nullptr;
@@ -84,7 +85,7 @@ int grow_host(vtq_ctx* c, void*& p, size_t& cap, size_t bytes) {
 
 // Shape of one dtype arm after validation.
 struct Plan {
-    enum Kind { kQ4KInt, kQ6KInt, kCanon } kind = kCanon;
+    enum Kind { kQ4KInt, kQ4KGemm, kQ6KInt, kCanon } kind = kCanon;
     vtq::CanonFormat fmt = vtq::kCanonQ8_0;
     size_t row_bytes = 0;
     size_t w_need = 0;  // bytes of w the kernels read
@@ -121,7 +122,9 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
                                                                : "linear_q4_k_integer_parallel: weight shape");
             if (in_feat > (size_t)vtq::kquant_max_in_feat())
                 return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 32768 for k-quant GEMV");
-            p->kind = Plan::kQ4KInt;
+            p->kind = (batch >= (size_t)vtq::kGemmMinBatch && in_feat <= (size_t)vtq::q4k_gemm_max_in_feat())
+                          ? Plan::kQ4KGemm
+                          : Plan::kQ4KInt;
         } else {
             return set_err(c, VTQ_E_INVALID_ARGUMENT, "vtq: unknown regime");
         }
@@ -189,6 +192,13 @@ int run_plan(vtq_ctx* c, const Plan& p, const float* dx, const uint8_t* dw, floa
         e = vtq::launch_fill(dy, batch * out_feat, 0.0f, s);
         return e == hipSuccess ? VTQ_OK : hip_fail(c, e, "fill");
     }
+    if (p.kind == Plan::kQ4KGemm) {
+        // rows of 128 tokens per grid.y: 65535 * 128 covers any batch up to INT_MAX / 2
+        int rc = grow_dev(c, c->ws, vtq::q4k_gemm_workspace_bytes((int)batch, (int)in_feat));
+        if (rc) return rc;
+        e = vtq::launch_q4k_gemm(dx, dw, dy, (int)batch, (int)in_feat, (int)out_feat, c->ws.ptr, s);
+        return e == hipSuccess ? VTQ_OK : hip_fail(c, e, "kernel launch");
+    }
     const size_t kMaxGridY = 65535;
     for (size_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
         const int nb = (int)(batch - b0 < kMaxGridY ? batch - b0 : kMaxGridY);
@@ -197,6 +207,8 @@ int run_plan(vtq_ctx* c, const Plan& p, const float* dx, const uint8_t* dw, floa
         switch (p.kind) {
         case Plan::kQ4KInt:
             e = vtq::launch_q4k_gemv(xb, dw, yb, nb, (int)in_feat, (int)out_feat, c->num_cus, s);
+            break;
+        case Plan::kQ4KGemm:
             break;
         case Plan::kQ6KInt:
             e = vtq::launch_q6k_gemv(xb, dw, yb, nb, (int)in_feat, (int)out_feat, c->num_cus, s);
@@ -312,6 +324,7 @@ void vtq_destroy(vtq_ctx* c) {
     for (auto& kv : c->weights) (void)hipFree(kv.second.dptr);
     if (c->dx.ptr) (void)hipFree(c->dx.ptr);
     if (c->dy.ptr) (void)hipFree(c->dy.ptr);
+    if (c->ws.ptr) (void)hipFree(c->ws.ptr);
     if (c->hx) (void)hipHostFree(c->hx);
     if (c->hy) (void)hipHostFree(c->hy);
     if (c->stream) (void)hipStreamDestroy(c->stream);

@@ -24,4 +24,12 @@ hipError_t launch_canon_gemv(CanonFormat fmt, const float* x, const uint8_t* w, 
                              int batch, int in_feat, int out_feat, int num_cus, hipStream_t stream);
 hipError_t launch_fill(float* y, size_t n, float v, hipStream_t stream);
 
+// Prefill GEMM (batch >= kGemmMinBatch): activation pre-pass into `workspace`
+// (q4k_gemm_workspace_bytes) followed by the i8-MFMA kernel.
+constexpr int kGemmMinBatch = 32;
+size_t q4k_gemm_workspace_bytes(int batch, int in_feat);
+int q4k_gemm_max_in_feat();
+hipError_t launch_q4k_gemm(const float* x, const uint8_t* w, float* y, int batch, int in_feat, int out_feat,
+                           void* workspace, hipStream_t stream);
+
 }  // namespace vtq
