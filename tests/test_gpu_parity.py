@@ -135,6 +135,13 @@ def test_kquant_unrestricted_bytes(ctx):
     check(ctx, vtq.Q6_K, 0, x, synth.random_bytes(out_f * 8 * 210, 6), 1, in_f, out_f)
 
 
+def test_q4k_prefill_gemm_unrestricted_bytes(ctx):
+    # the GEMM's scale decode and f16 conversion on arbitrary block bytes
+    batch, in_f, out_f = 40, 2048, 72
+    x = synth.activations(batch * in_f, seed=98)
+    check(ctx, vtq.Q4_K, 0, x, synth.random_bytes(out_f * 8 * 144, 7), batch, in_f, out_f)
+
+
 def test_activation_edge_cases(ctx):
     # zero blocks, NaN, +-Inf, subnormals, huge values, exact ties, -0.0
     in_f, out_f = 8 * 256, 40

@@ -21,10 +21,8 @@
 // digits of R, each built left to right as parts arrive.
 //
 // Tile: a workgroup of 4 waves owns 32 weight rows x 128 tokens; wave w owns
-// tokens 32w..32w+31 of the tile.  Per super-block the workgroup stages the
-// 32 rows' 144-byte blocks in LDS and builds the MFMA weight operands there
-// once; each wave reads its token operands (the pre-quantized activation)
-// straight from global memory.
+// tokens 32w..32w+31 of the tile.  The activation pre-pass writes the token
+// codes in the MFMA operand order, so each wave's operand loads are contiguous.
 #include "vtq_device.h"
 #include "vtq_kernels.h"
 
@@ -35,154 +33,237 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 
 // ------------------------------------------------ activation pre-pass
 
+// Workspace layout, in tiles of 32 tokens (Mp = batch rounded up to 32; the
+// padding tokens hold zeros):
+//   xqt [Mp/32][R][8][64] x 16 B   k-step j, lane 32g+n: codes 32j+16g .. +15
+//                                   of token 32T+n (the MFMA B operand, so one
+//                                   wave reads 1 KB contiguous per k-step)
+//   xdt [Mp/32][R][32] f32          d of each (token, super-block)
+//   xbt [Mp/32][R][32] x 16 B       bl[8] = bsum & 63, bh[8] = bsum >> 6
+struct GemmWs {
+    v4i* xqt;
+    float* xdt;
+    v4i* xbt;
+};
+
+inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+inline GemmWs gemm_ws(void* base, int Mp, int R) {
+    uint8_t* p = static_cast<uint8_t*>(base);
+    GemmWs w;
+    w.xqt = reinterpret_cast<v4i*>(p);
+    p += align256((size_t)Mp * R * 256);
+    w.xdt = reinterpret_cast<float*>(p);
+    p += align256((size_t)Mp * R * 4);
+    w.xbt = reinterpret_cast<v4i*>(p);
+    return w;
+}
+
 // quantize_block_q8 (src/ops/quant.rs:750-771) of every 256-block of every
-// batch row: one wave per (row, block).  Writes the codes row-major
-// [M][K], d [M][R], and the split sub-block sums [M][R][16] = bl[8], bh[8].
-__global__ __launch_bounds__(256) void act_quant_rows_kernel(const float* __restrict__ x, int8_t* __restrict__ xq,
-                                                              float* __restrict__ xd, int8_t* __restrict__ xb,
-                                                              int R, int M) {
+// batch row: one wave per (token, super-block), written in the tiled layout.
+__global__ __launch_bounds__(256) void act_quant_tiles_kernel(const float* __restrict__ x, GemmWs ws, int R, int M,
+                                                              int Mp) {
     const int lane = threadIdx.x & 63;
     const long blk = (long)blockIdx.x * 4 + wave_id();
-    if (blk >= (long)R * M) return;
+    if (blk >= (long)Mp * R) return;
     const long b = blk / R, s = blk % R;
-    const long K = (long)R * 256;
-    const float4 v = reinterpret_cast<const float4*>(x + b * K + s * 256)[lane];
-    uint32_t packed;
-    int s16, s32;
-    const float d = quant_block_wave(v, &packed, &s16, &s32);
-    reinterpret_cast<uint32_t*>(xq + b * K + s * 256)[lane] = packed;
-    if (lane == 0) xd[b * R + s] = d;
+    const long tile = (b >> 5) * R + s;
+    const int n = (int)(b & 31);
+    uint32_t packed = 0;
+    int s16 = 0, s32 = 0;
+    float d = 0.0f;
+    if (b < M) {  // uniform per wave
+        const float4 v = reinterpret_cast<const float4*>(x + b * (long)R * 256 + s * 256)[lane];
+        d = quant_block_wave(v, &packed, &s16, &s32);
+    }
+    // lane holds elements 4*lane .. +3: k-step j = lane/8, half g = (lane/4)&1
+    const int j = lane >> 3, g = (lane >> 2) & 1;
+    uint8_t* dst = reinterpret_cast<uint8_t*>(ws.xqt + (tile * 8 + j) * 64 + 32 * g + n) + 4 * (lane & 3);
+    *reinterpret_cast<uint32_t*>(dst) = packed;
+    if (lane == 0) ws.xdt[tile * 32 + n] = d;
     if ((lane & 7) == 0) {
-        const int j = lane >> 3;
-        int8_t* o = xb + (b * R + s) * 16;
-        o[j] = (int8_t)(s32 & 63);       // bl
-        o[8 + j] = (int8_t)(s32 >> 6);   // bh (arithmetic shift: s32 = 64*bh + bl)
+        int8_t* o = reinterpret_cast<int8_t*>(ws.xbt + tile * 32 + n);
+        o[j] = (int8_t)(s32 & 63);      // bl
+        o[8 + j] = (int8_t)(s32 >> 6);  // bh (arithmetic shift: s32 = 64*bh + bl)
     }
 }
 
 // ---------------------------------------------------------------- GEMM
 
-constexpr int kTO = 32;   // weight rows per workgroup
-constexpr int kTB = 128;  // tokens per workgroup (4 waves x 32)
+constexpr int kTO = 32;        // weight rows per workgroup
+constexpr int kTB = 128;       // tokens per workgroup (4 waves x 32)
+constexpr int kChunkM = 8192;  // tokens per launch pair (bounds the workspace)
 
+typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+
+// Byte-wise product of four nibbles (each <= 15) with m <= 7: every byte
+// stays below 256, so one packed 16-bit multiply carries nothing across bytes.
+__device__ __forceinline__ int nib_mul(uint32_t w, us2 m) {
+    return (int)__builtin_bit_cast(uint32_t, __builtin_bit_cast(us2, w) * m);
+}
+
+// One workgroup: 32 weight rows x 128 tokens; wave w owns tokens 32w..32w+31.
+// Per super-block the workgroup builds the weight operands once in LDS
+// (double-buffered: one barrier per super-block), while each wave's token
+// operands and the next super-block's weight bytes are prefetched into
+// registers during the current super-block's MFMAs and epilogue.
 template <int LV>
-__global__ __launch_bounds__(256, 2) void q4k_gemm_kernel(const uint8_t* __restrict__ W,
-                                                          const int8_t* __restrict__ xq,
-                                                          const float* __restrict__ xd,
-                                                          const int8_t* __restrict__ xb, float* __restrict__ y,
-                                                          int R, int N, int M) {
-    __shared__ __align__(16) uint8_t raw[kTO * 144];  // 32 rows' blocks of super-block s
-    __shared__ v4i opA1[8][64];                         // weight operands per k-step (sub-block) and lane
-    __shared__ v4i opA0[8][64];
-    __shared__ v4i opAm[64];                            // min-term operand
-    __shared__ float dsh[kTO], dminsh[kTO];
+__global__ __launch_bounds__(256, 2) void q4k_gemm_kernel(const uint8_t* __restrict__ W, GemmWs ws,
+                                                          float* __restrict__ y, int R, int N, int M, int NR,
+                                                          int TT) {
+    __shared__ v4i opA1[2][8][64];  // weight operands per buffer, k-step (sub-block) and lane
+    __shared__ v4i opA0[2][8][64];
+    __shared__ uint2 opAm[2][64];   // min-term operand: bytes m_0..m_7 of each row; lanes 32..63 zero
+    __shared__ float dd[2][2][32];  // d, dmin of each row
 
     const int t = threadIdx.x, lane = t & 63, wave = wave_id();
-    const int o0 = blockIdx.x * kTO;
+    // Tile order: workgroup i runs on XCD i % 8, so the TT token tiles of one
+    // row tile are given consecutive slots of one XCD and share its L2.
+    const int id = blockIdx.x, full = (NR / 8) * 8 * TT;
+    int rt, tt;
+    if (id < full) {
+        const int k = id >> 3;
+        rt = (k / TT) * 8 + (id & 7);
+        tt = k % TT;
+    } else {
+        rt = (NR / 8) * 8 + (id - full) / TT;
+        tt = (id - full) % TT;
+    }
+    const int o0 = rt * kTO;
     const int g = lane >> 5, n = lane & 31;
-    const int tok = min(blockIdx.y * kTB + wave * 32 + n, M - 1);  // clamped: tail tokens are discarded
-    const long K = (long)R * 256;
-    const size_t row_bytes = (size_t)R * 144;
+    const int Tw = tt * 4 + wave;                  // this wave's 32-token tile
+    const int T = min(Tw, (M + 31) / 32 - 1);      // past-the-end waves recompute the last tile
+    const v4i* xq_w = ws.xqt + (size_t)T * R * 512 + lane;
+    const v4i* xb_w = ws.xbt + (size_t)T * R * 32 + n;
+    const float* xd_w = ws.xdt + (size_t)T * R * 32 + n;
 
+    // operand builder: thread (row br, sub-block bj)
+    const int br = lane & 31, bj = t >> 5;
+    const uint8_t* wrow = W + (size_t)min(o0 + br, N - 1) * ((size_t)R * 144);
+    const uint32_t nsh = 4 * (bj & 1), ssh = 8 * (bj & 3);
+
+    uint4 h, q0, q1;
+    auto wload = [&](int s) {
+        const uint8_t* blk = wrow + (size_t)s * 144;
+        h = *reinterpret_cast<const uint4*>(blk);
+        const uint4* qp = reinterpret_cast<const uint4*>(blk + 16 + 32 * (bj >> 1));
+        q0 = qp[0];
+        q1 = qp[1];
+    };
+    auto build = [&](int buf) {
+        // get_scale_min_k4 (src/ops/quant.rs:267-276) for sub-block bj: scale bytes 0..11 = h.y, h.z, h.w
+        const uint32_t by = (h.y >> ssh) & 255u, bz = (h.z >> ssh) & 255u, bw = (h.w >> ssh) & 255u;
+        const uint32_t up = bj >= 4 ? ~0u : 0u;  // sub-blocks 4..7 take the split encoding
+        const uint32_t sc = ((by & 63u) & ~up) | (((bw & 15u) | ((by >> 6) << 4)) & up);
+        const uint32_t mn = ((bz & 63u) & ~up) | (((bw >> 4) | ((bz >> 6) << 4)) & up);
+        const us2 mh = {(unsigned short)(sc >> 3), (unsigned short)(sc >> 3)};
+        const us2 ml = {(unsigned short)(sc & 7u), (unsigned short)(sc & 7u)};
+        const uint32_t w[8] = {(q0.x >> nsh) & 0x0F0F0F0Fu, (q0.y >> nsh) & 0x0F0F0F0Fu, (q0.z >> nsh) & 0x0F0F0F0Fu,
+                               (q0.w >> nsh) & 0x0F0F0F0Fu, (q1.x >> nsh) & 0x0F0F0F0Fu, (q1.y >> nsh) & 0x0F0F0F0Fu,
+                               (q1.z >> nsh) & 0x0F0F0F0Fu, (q1.w >> nsh) & 0x0F0F0F0Fu};
+        opA1[buf][bj][br] = v4i{nib_mul(w[0], mh), nib_mul(w[1], mh), nib_mul(w[2], mh), nib_mul(w[3], mh)};
+        opA1[buf][bj][br + 32] = v4i{nib_mul(w[4], mh), nib_mul(w[5], mh), nib_mul(w[6], mh), nib_mul(w[7], mh)};
+        opA0[buf][bj][br] = v4i{nib_mul(w[0], ml), nib_mul(w[1], ml), nib_mul(w[2], ml), nib_mul(w[3], ml)};
+        opA0[buf][bj][br + 32] = v4i{nib_mul(w[4], ml), nib_mul(w[5], ml), nib_mul(w[6], ml), nib_mul(w[7], ml)};
+        reinterpret_cast<uint8_t*>(&opAm[buf][br])[bj] = (uint8_t)mn;
+        if (bj < 2) dd[buf][bj][br] = f16_to_f32_sel((h.x >> (16 * bj)) & 0xFFFFu);  // wave 0 only
+    };
+
+    // Token operands of the current super-block (reloaded for the next one
+    // as soon as the current MFMAs are issued).
+    v4i bop[8], bsv;
+    float dx;
+    auto tload = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) bop[j] = xq_w[(s * 8 + j) * 64];
+        bsv = xb_w[s * 32];
+        dx = xd_w[s * 32];
+    };
+
+    // One super-block s from LDS buffer `buf`; prefetches the tokens of s+1
+    // and the weights of s+2, and builds the weight operands of s+1 into the
+    // other buffer.  Writes the per-(row, token) parts of s to p.  (Past the
+    // end the loads repeat the last super-block: every load is
+    // unconditional, so the wait counts stay exact across the back edge.)
+    auto sblock = [&](int s, int buf, float (&p)[16]) __attribute__((always_inline)) {
+        // acc = 8*C1 + C0 from two interleaved accumulator chains; token
+        // register j is reloaded for super-block s+1 as soon as its two
+        // MFMAs have been issued.  accm = 64*Ch + Cl is chained through one
+        // accumulator (Ch scaled in place becomes the C input of Cl).
+        const int sn = min(s + 1, R - 1);
+        v16i c1 = {}, c0 = {}, cm = {};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(opA1[buf][j][lane], bop[j], c1, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(opA0[buf][j][lane], bop[j], c0, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            bop[j] = xq_w[(sn * 8 + j) * 64];
+        }
+        const uint2 amv = opAm[buf][lane];  // zero for lanes 32..63
+        const v4i am = v4i{(int)amv.x, (int)amv.y, 0, 0};
+        const v4i bh = g == 0 ? v4i{bsv.z, bsv.w, 0, 0} : v4i{0, 0, 0, 0};
+        const v4i bl = g == 0 ? v4i{bsv.x, bsv.y, 0, 0} : v4i{0, 0, 0, 0};
+        cm = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bh, cm, 0, 0, 0);
+        const float dxs = dx;
+        __builtin_amdgcn_sched_barrier(0);
+        bsv = xb_w[sn * 32];
+        dx = xd_w[sn * 32];
+        int acc[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[i] = 8 * c1[i] + c0[i];
+#pragma unroll
+        for (int i = 0; i < 16; i++) cm[i] *= 64;
+        cm = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bl, cm, 0, 0, 0);
+        // epilogue (src/ops/quant.rs:849-898): element i of this lane is row 8*(i/4) + 4*g + i%4, token n
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 dv = *reinterpret_cast<const float4*>(&dd[buf][0][8 * q + 4 * g]);
+            const float4 mv = *reinterpret_cast<const float4*>(&dd[buf][1][8 * q + 4 * g]);
+            const float dr[4] = {dv.x, dv.y, dv.z, dv.w}, mr[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = 4 * q + e;
+                const float t1 = (dr[e] * dxs) * (float)acc[i];
+                const float t2 = (mr[e] * dxs) * (float)cm[i];
+                p[i] = t1 - t2;
+            }
+        }
+        build(buf ^ 1);
+        wload(min(s + 2, R - 1));
+        __syncthreads();
+    };
+
+    // fixed_tree (src/ops/quant.rs:461-476) streamed as a binary counter:
+    // level l holds the completed 2^l-block, combined as the left operand
+    // with the block that completes it.  After leaf s, the levels below
+    // L = (trailing ones of s) merge into level L; L is uniform, and each
+    // case writes its chain straight into its level (no register shuffles).
     float stk[LV][16];
 #pragma unroll
     for (int l = 0; l < LV; l++)
 #pragma unroll
         for (int i = 0; i < 16; i++) stk[l][i] = 0.0f;
 
+    if (t < 64) opAm[t >> 5][32 + (t & 31)] = make_uint2(0u, 0u);
+    tload(0);
+    wload(0);
+    build(0);
+    wload(min(1, R - 1));
+    __syncthreads();
+
     for (int s = 0; s < R; s++) {
-        // token operands of this super-block (global, issued before the LDS phase)
-        const v4i* xrow = reinterpret_cast<const v4i*>(xq + (long)tok * K + (long)s * 256);
-        v4i bop[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) bop[j] = xrow[2 * j + g];  // elements 32j + 16g .. +16
-        const int8_t* bs = xb + ((long)tok * R + s) * 16;
-        const int2 bsl = *reinterpret_cast<const int2*>(bs);      // bl[0..8)
-        const int2 bsh = *reinterpret_cast<const int2*>(bs + 8);  // bh[0..8)
-        const float dx = xd[(long)tok * R + s];
-
-        __syncthreads();  // previous super-block's operands are consumed
-        // stage 32 rows x 144 B (288 chunks of 16 B)
-        for (int c = t; c < kTO * 9; c += 256) {
-            const int r = c / 9, q = c % 9;
-            const int orow = min(o0 + r, N - 1);
-            *reinterpret_cast<uint4*>(raw + r * 144 + q * 16) =
-                *reinterpret_cast<const uint4*>(W + (size_t)orow * row_bytes + (size_t)s * 144 + q * 16);
-        }
-        __syncthreads();
-        // build operands: thread (row r = t%32, sub-block j = t/32) writes the two lanes (r, g=0/1)
-        {
-            const int r = t & 31, j = t >> 5;
-            const uint8_t* blk = raw + r * 144;
-            const uint8_t* sb = blk + 4;
-            uint32_t sc, mn;
-            if (j < 4) {
-                sc = sb[j] & 63u;
-                mn = sb[j + 4] & 63u;
-            } else {
-                sc = (sb[j + 4] & 15u) | ((uint32_t)(sb[j - 4] >> 6) << 4);
-                mn = (uint32_t)(sb[j + 4] >> 4) | ((uint32_t)(sb[j] >> 6) << 4);
-            }
-            const uint32_t sh = sc >> 3, sl = sc & 7u;
-            const uint4* q4 = reinterpret_cast<const uint4*>(blk + 16 + 32 * (j >> 1));
-            const bool hi = (j & 1) != 0;
-#pragma unroll
-            for (int gg = 0; gg < 2; gg++) {
-                const uint4 qv = q4[gg];
-                const uint32_t w0 = (hi ? qv.x >> 4 : qv.x) & 0x0F0F0F0Fu, w1 = (hi ? qv.y >> 4 : qv.y) & 0x0F0F0F0Fu;
-                const uint32_t w2 = (hi ? qv.z >> 4 : qv.z) & 0x0F0F0F0Fu, w3 = (hi ? qv.w >> 4 : qv.w) & 0x0F0F0F0Fu;
-                // byte-wise products stay below 256: no carry between bytes
-                opA1[j][r + 32 * gg] = v4i{(int)(w0 * sh), (int)(w1 * sh), (int)(w2 * sh), (int)(w3 * sh)};
-                opA0[j][r + 32 * gg] = v4i{(int)(w0 * sl), (int)(w1 * sl), (int)(w2 * sl), (int)(w3 * sl)};
-            }
-            // min-term operand: lane (r, g=0) bytes 0..7 = m_0..m_7 (one byte per thread j)
-            reinterpret_cast<uint8_t*>(&opAm[r])[j] = (uint8_t)mn;
-            reinterpret_cast<uint8_t*>(&opAm[r])[8 + j] = 0;
-            reinterpret_cast<uint8_t*>(&opAm[r + 32])[j] = 0;
-            reinterpret_cast<uint8_t*>(&opAm[r + 32])[8 + j] = 0;
-            if (j == 0) {
-                dsh[r] = f16_to_f32(blk[0] | (blk[1] << 8));
-                dminsh[r] = f16_to_f32(blk[2] | (blk[3] << 8));
-            }
-        }
-        __syncthreads();
-
-        v16i c1 = {}, c0 = {}, cl = {}, ch = {};
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(opA1[j][lane], bop[j], c1, 0, 0, 0);
-            c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(opA0[j][lane], bop[j], c0, 0, 0, 0);
-        }
-        const v4i am = opAm[lane];
-        const v4i bl = g == 0 ? v4i{bsl.x, bsl.y, 0, 0} : v4i{0, 0, 0, 0};
-        const v4i bh = g == 0 ? v4i{bsh.x, bsh.y, 0, 0} : v4i{0, 0, 0, 0};
-        cl = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bl, cl, 0, 0, 0);
-        ch = __builtin_amdgcn_mfma_i32_32x32x32_i8(am, bh, ch, 0, 0, 0);
-
-        // epilogue: element i of this lane is row 8*(i/4) + 4*g + i%4, token n
         float p[16];
+        sblock(s, s & 1, p);
+        const int L = __builtin_ctz(~s);
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int r = 8 * (i >> 2) + 4 * g + (i & 3);
-            const int acc = 8 * c1[i] + c0[i];
-            const int accm = 64 * ch[i] + cl[i];
-            const float t1 = (dsh[r] * dx) * (float)acc;
-            const float t2 = (dminsh[r] * dx) * (float)accm;
-            p[i] = t1 - t2;
-        }
-        // fixed_tree, streamed: combine with the stored block of each level while bit l of s is set
-        bool carry = true;
+        for (int LL = 0; LL < LV; LL++) {
+            if (L == LL) {
 #pragma unroll
-        for (int l = 0; l < LV; l++) {
-            if (carry) {
-                if ((s >> l) & 1) {
+                for (int l = 0; l < LL; l++)
 #pragma unroll
                     for (int i = 0; i < 16; i++) p[i] = stk[l][i] + p[i];
-                } else {
 #pragma unroll
-                    for (int i = 0; i < 16; i++) stk[l][i] = p[i];
-                    carry = false;
-                }
+                for (int i = 0; i < 16; i++) stk[LL][i] = p[i];
             }
         }
     }
@@ -197,15 +278,16 @@ __global__ __launch_bounds__(256, 2) void q4k_gemm_kernel(const uint8_t* __restr
             have = true;
         }
     }
-    const int tok_real = blockIdx.y * kTB + wave * 32 + n;
-    if (tok_real < M) {
-        float* yrow = y + (long)tok_real * N;
+    const int tok = Tw * 32 + n;
+    if (tok < M) {
+        float* yrow = y + (size_t)tok * N;
+        const bool vec = (N & 3) == 0;
 #pragma unroll
         for (int q = 0; q < 4; q++) {
-            const int r = 8 * q + 4 * g;
-            const int o = o0 + r;
-            if (o + 3 < N) {
-                *reinterpret_cast<float4*>(yrow + o) = make_float4(r16[4 * q], r16[4 * q + 1], r16[4 * q + 2], r16[4 * q + 3]);
+            const int o = o0 + 8 * q + 4 * g;
+            if (vec && o + 3 < N) {
+                *reinterpret_cast<float4*>(yrow + o) =
+                    make_float4(r16[4 * q], r16[4 * q + 1], r16[4 * q + 2], r16[4 * q + 3]);
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; e++)
@@ -216,38 +298,48 @@ __global__ __launch_bounds__(256, 2) void q4k_gemm_kernel(const uint8_t* __restr
 }
 
 size_t q4k_gemm_workspace_bytes(int batch, int in_feat) {
+    const int Mp = (min(batch, kChunkM) + 31) / 32 * 32;
     const size_t R = in_feat / 256;
-    return ((size_t)batch * in_feat + 255) / 256 * 256 + ((size_t)batch * R * 4 + 255) / 256 * 256 +
-           (size_t)batch * R * 16 + 256;
+    return align256((size_t)Mp * R * 256) + align256((size_t)Mp * R * 4) + (size_t)Mp * R * 16;
 }
 
 int q4k_gemm_max_in_feat() { return 127 * 256; }
 
+template <int LV>
+static void launch_gemm_lv(dim3 grid, hipStream_t stream, const uint8_t* w, GemmWs ws, float* y, int R, int N, int M,
+                           int NR, int TT) {
+    hipLaunchKernelGGL(q4k_gemm_kernel<LV>, grid, dim3(256), 0, stream, w, ws, y, R, N, M, NR, TT);
+}
+
 hipError_t launch_q4k_gemm(const float* x, const uint8_t* w, float* y, int batch, int in_feat, int out_feat,
                            void* workspace, hipStream_t stream) {
     const int R = in_feat / 256;
-    uint8_t* ws = static_cast<uint8_t*>(workspace);
-    int8_t* xq = reinterpret_cast<int8_t*>(ws);
-    float* xd = reinterpret_cast<float*>(ws + ((size_t)batch * in_feat + 255) / 256 * 256);
-    int8_t* xb = reinterpret_cast<int8_t*>(reinterpret_cast<uint8_t*>(xd) + ((size_t)batch * R * 4 + 255) / 256 * 256);
-    const long blocks = (long)batch * R;
-    hipLaunchKernelGGL(act_quant_rows_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, stream, x, xq, xd,
-                       xb, R, batch);
-    if (hipError_t e = hipGetLastError()) return e;
-    dim3 grid((unsigned)((out_feat + kTO - 1) / kTO), (unsigned)((batch + kTB - 1) / kTB), 1);
     int lv = 0;
     while ((1 << lv) <= R) lv++;  // bit length of R: R < 2^lv
-    switch (lv) {
-    case 1: hipLaunchKernelGGL(q4k_gemm_kernel<1>, grid, dim3(256), 0, stream, w, xq, xd, xb, y, R, out_feat, batch); break;
-    case 2: hipLaunchKernelGGL(q4k_gemm_kernel<2>, grid, dim3(256), 0, stream, w, xq, xd, xb, y, R, out_feat, batch); break;
-    case 3: hipLaunchKernelGGL(q4k_gemm_kernel<3>, grid, dim3(256), 0, stream, w, xq, xd, xb, y, R, out_feat, batch); break;
-    case 4: hipLaunchKernelGGL(q4k_gemm_kernel<4>, grid, dim3(256), 0, stream, w, xq, xd, xb, y, R, out_feat, batch); break;
-    case 5: hipLaunchKernelGGL(q4k_gemm_kernel<5>, grid, dim3(256), 0, stream, w, xq, xd, xb, y, R, out_feat, batch); break;
-    case 6: hipLaunchKernelGGL(q4k_gemm_kernel<6>, grid, dim3(256), 0, stream, w, xq, xd, xb, y, R, out_feat, batch); break;
-    case 7: hipLaunchKernelGGL(q4k_gemm_kernel<7>, grid, dim3(256), 0, stream, w, xq, xd, xb, y, R, out_feat, batch); break;
-    default: return hipErrorInvalidValue;
+    if (lv < 1 || lv > 7) return hipErrorInvalidValue;
+    const int NR = (out_feat + kTO - 1) / kTO;
+    for (int b0 = 0; b0 < batch; b0 += kChunkM) {
+        const int M = min(batch - b0, kChunkM), Mp = (M + 31) / 32 * 32;
+        const GemmWs ws = gemm_ws(workspace, Mp, R);
+        const long blocks = (long)Mp * R;
+        hipLaunchKernelGGL(act_quant_tiles_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, stream,
+                           x + (size_t)b0 * in_feat, ws, R, M, Mp);
+        if (hipError_t e = hipGetLastError()) return e;
+        const int TT = (M + kTB - 1) / kTB;
+        const dim3 grid((unsigned)NR * (unsigned)TT);
+        float* yb = y + (size_t)b0 * out_feat;
+        switch (lv) {
+        case 1: launch_gemm_lv<1>(grid, stream, w, ws, yb, R, out_feat, M, NR, TT); break;
+        case 2: launch_gemm_lv<2>(grid, stream, w, ws, yb, R, out_feat, M, NR, TT); break;
+        case 3: launch_gemm_lv<3>(grid, stream, w, ws, yb, R, out_feat, M, NR, TT); break;
+        case 4: launch_gemm_lv<4>(grid, stream, w, ws, yb, R, out_feat, M, NR, TT); break;
+        case 5: launch_gemm_lv<5>(grid, stream, w, ws, yb, R, out_feat, M, NR, TT); break;
+        case 6: launch_gemm_lv<6>(grid, stream, w, ws, yb, R, out_feat, M, NR, TT); break;
+        default: launch_gemm_lv<7>(grid, stream, w, ws, yb, R, out_feat, M, NR, TT); break;
+        }
+        if (hipError_t e = hipGetLastError()) return e;
     }
-    return hipGetLastError();
+    return hipSuccess;
 }
 
 }  // namespace vtq

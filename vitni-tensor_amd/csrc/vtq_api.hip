@@ -193,7 +193,7 @@ int run_plan(vtq_ctx* c, const Plan& p, const float* dx, const uint8_t* dw, floa
         return e == hipSuccess ? VTQ_OK : hip_fail(c, e, "fill");
     }
     if (p.kind == Plan::kQ4KGemm) {
-        // rows of 128 tokens per grid.y: 65535 * 128 covers any batch up to INT_MAX / 2
+        // the launcher walks the batch in chunks that fit the workspace
         int rc = grow_dev(c, c->ws, vtq::q4k_gemm_workspace_bytes((int)batch, (int)in_feat));
         if (rc) return rc;
         e = vtq::launch_q4k_gemm(dx, dw, dy, (int)batch, (int)in_feat, (int)out_feat, c->ws.ptr, s);

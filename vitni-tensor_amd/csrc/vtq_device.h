@@ -47,6 +47,13 @@ __device__ __forceinline__ float f16_hw(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
+// f16_to_f32's exact bits, branch-free: v_cvt_f32_f16 for every non-NaN
+// code, and the payload-shifting formula selected for a NaN.
+__device__ __forceinline__ float f16_to_f32_sel(uint32_t h) {
+    const uint32_t nan_bits = ((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x3FFu) << 13);
+    return (h & 0x7FFFu) > 0x7C00u ? __uint_as_float(nan_bits) : f16_hw(h);
+}
+
 // Rust `(t as i32).clamp(-127, 127)` for the activation quantizer: NaN -> 0,
 // truncation toward zero, saturation (src/ops/quant.rs:766).  Branch-free:
 // clamp in float (exact), truncate (exact for |c| <= 127), and select 0
