@@ -112,7 +112,9 @@ int vtq_release_weights(vtq_ctx *ctx, const uint8_t *w);
  * Same computation as vtq_linear, but d_x, d_w, d_y are device memory on the
  * context's device and the work is enqueued on `stream` (a hipStream_t, NULL
  * for the null stream) without synchronising.  d_x and d_w must be 16-byte
- * aligned.  This is what a device-resident forward step calls; it replaces
+ * aligned, and d_w readable up to the next multiple of 16 bytes past w_len
+ * (every hipMalloc or torch device allocation is: the kernels fetch whole
+ * 16-byte chunks and ignore the bytes past the blob).  This is what a device-resident forward step calls; it replaces
  * the same linear_dispatch arm as vtq_linear.  Calls that overlap in time on
  * one context race on the context's workspace. */
 int vtq_linear_device(vtq_ctx *ctx, int ggml_type, int regime, const float *d_x,

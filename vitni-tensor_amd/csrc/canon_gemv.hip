@@ -15,6 +15,8 @@
 #include "vtq_device.h"
 #include "vtq_kernels.h"
 
+#include <type_traits>
+
 namespace vtq {
 
 constexpr int kChunk = 8192;
@@ -26,9 +28,10 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *reinterpr
 // elements kBlock*bi + j + 8m, m = 0 .. kBlock/8 - 1.
 struct DecQ8_0 {  // src/ops/quant.rs:193-210
     static constexpr int kBlock = 32;
+    static constexpr int kWinBytes = 8 * 34;  // bytes of 256 elements
     __device__ static void decode(const uint8_t* row, int bi, int j, float* w) {
         const uint8_t* blk = row + 34 * bi;
-        const float d = f16_to_f32(ld_u16(blk));
+        const float d = f16_to_f32_sel(ld_u16(blk));
 #pragma unroll
         for (int m = 0; m < 4; m++) w[m] = d * (float)(int8_t)blk[2 + j + 8 * m];
     }
@@ -36,9 +39,10 @@ struct DecQ8_0 {  // src/ops/quant.rs:193-210
 
 struct DecQ5_0 {  // src/ops/quant.rs:160-186
     static constexpr int kBlock = 32;
+    static constexpr int kWinBytes = 8 * 22;
     __device__ static void decode(const uint8_t* row, int bi, int j, float* w) {
         const uint8_t* blk = row + 22 * bi;
-        const float d = f16_to_f32(ld_u16(blk));
+        const float d = f16_to_f32_sel(ld_u16(blk));
         const uint32_t qh = ld_u16(blk + 2) | (ld_u16(blk + 4) << 16);
         const uint8_t* qs = blk + 6;
 #pragma unroll
@@ -53,9 +57,10 @@ struct DecQ5_0 {  // src/ops/quant.rs:160-186
 
 struct DecQ4_0 {  // src/ops/quant.rs:91-111 (element 2k low nibble, 2k+1 high)
     static constexpr int kBlock = 32;
+    static constexpr int kWinBytes = 8 * 18;
     __device__ static void decode(const uint8_t* row, int bi, int j, float* w) {
         const uint8_t* blk = row + 18 * bi;
-        const float d = f16_to_f32(ld_u16(blk));
+        const float d = f16_to_f32_sel(ld_u16(blk));
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const int e = j + 8 * m;
@@ -68,11 +73,12 @@ struct DecQ4_0 {  // src/ops/quant.rs:91-111 (element 2k low nibble, 2k+1 high)
 
 struct DecQ4KFloat {  // src/ops/quant.rs:649-667: w = d1*q - m1f per sub-block
     static constexpr int kBlock = 32;
+    static constexpr int kWinBytes = 144;
     __device__ static void decode(const uint8_t* row, int bi, int j, float* w) {
         const int sb = bi >> 3, sj = bi & 7;
         const uint8_t* blk = row + 144 * sb;
-        const float d = f16_to_f32(ld_u16(blk));
-        const float dmin = f16_to_f32(ld_u16(blk + 2));
+        const float d = f16_to_f32_sel(ld_u16(blk));
+        const float dmin = f16_to_f32_sel(ld_u16(blk + 2));
         const uint8_t* s = blk + 4;
         uint32_t sc, mn;
         if (sj < 4) {
@@ -97,6 +103,7 @@ struct DecQ4KFloat {  // src/ops/quant.rs:649-667: w = d1*q - m1f per sub-block
 
 struct DecF32 {  // src/model/forward_quantized.rs:674-697
     static constexpr int kBlock = 8;
+    static constexpr int kWinBytes = 1024;
     __device__ static void decode(const uint8_t* row, int bi, int j, float* w) {
         w[0] = reinterpret_cast<const float*>(row)[8 * bi + j];
     }
@@ -140,6 +147,269 @@ __global__ __launch_bounds__(256) void canon_gemv_kernel(const float* __restrict
     if (c == 0 && j == 0 && o < out_feat) y[(size_t)blockIdx.y * out_feat + o] = v;
 }
 
+// Windowed producer/consumer form.  A row's 8 chains are 8 lanes, so a
+// 4096-row layer has only 32768 chains (512 waves): summing them is cheap,
+// decoding and multiplying 16.8M elements is not.  So one workgroup = one
+// consumer wave (8 groups of 8 chain lanes, as in canon_gemv_kernel) plus
+// eight producer waves.  The row data is walked in windows of 256 elements:
+//  * producers fetch each window's raw weight bytes (whole 16-byte chunks)
+//    and its x values four windows ahead in registers, stage them in LDS
+//    (x transposed chain-major), then decode and form the products
+//    x_i * w_i of the window: 512 units of 4 consecutive chain positions,
+//    one per producer lane;
+//  * the consumer adds the previous window's products into its chains in
+//    increasing element order (the reference's sequential lane chains).
+// Products of elements past a chunk's end are written as -0.0, which is the
+// exact additive identity, so every chain adds 32 values per window.  One
+// barrier per window; LDS buffers alternate by window parity.  All loads
+// are unconditional (clamped past the end), so the wait counts stay exact.
+// Weight chunks may read up to 15 bytes past the end of the blob, within
+// the caller's 16-byte-rounded allocation.
+template <class Dec, int CPW>
+struct PcWin {
+    static constexpr int kRows = 8 / CPW;
+    static constexpr int WB = Dec::kWinBytes;         // a multiple of 16 for every format
+    static constexpr int RAWB = (WB + 30) / 16 * 16;  // window + misalignment slack, whole chunks
+    static constexpr int NCH = RAWB / 16;             // 16-byte chunks per group window
+    static constexpr int NLOAD = 8 * NCH + 64 * CPW;  // chunks per window: weights, then x
+    static constexpr int NPW = 8;                     // producer waves
+    static constexpr int NP = 64 * NPW;               // producer lanes
+    static constexpr int UPL = 512 / NP;              // product units per producer lane
+    static constexpr int LPL = (NLOAD + NP - 1) / NP;  // chunk loads per producer lane
+    static constexpr int XS = 36;                     // chain stride (floats) of x and product windows
+    static constexpr int GS = 8 * XS;                 // group stride of the product window
+    static constexpr int EPB = Dec::kBlock / 8;       // chain elements per block
+    static_assert(WB % 16 == 0, "window byte size");
+
+    // one window's registers as one vector value (stays in registers)
+    typedef uint32_t Regs __attribute__((ext_vector_type(4 * LPL)));
+
+    // per producer lane, fixed for the whole row walk
+    struct Chunk {             // one 16-byte fetch per window
+        const uint8_t* base;   // address at window 0
+        int cap;               // last window index it may advance to
+        int step;              // bytes per window (weights) or 0 for x
+        int dst;               // LDS byte offset: raw, x (-1 - transposed slot) or spare
+    };
+    struct Unit {              // 4 consecutive chain positions of one group
+        int raw, xoff, poff;   // LDS offsets: block bytes of the group, x quad, product quad
+        int e0, ce;            // element of position 0 at window 0, chunk end
+        int blk, j;            // block index in the window (f32: first of 4), chain
+        bool live;
+    };
+};
+
+template <class Dec, int CPW>
+__global__ __launch_bounds__(576) void canon_pc_kernel(const float* __restrict__ x, const uint8_t* __restrict__ W,
+                                                       size_t row_bytes, size_t wbytes, float* __restrict__ y, int n,
+                                                       int out_feat, int nchunks, int nwin) {
+    using Wn = PcWin<Dec, CPW>;
+    constexpr int RAWB = Wn::RAWB, XS = Wn::XS, GS = Wn::GS, NCH = Wn::NCH, LPL = Wn::LPL, WB = Wn::WB;
+    constexpr int NLOAD = Wn::NLOAD, EPB = Wn::EPB, NP = Wn::NP, UPL = Wn::UPL;
+    constexpr int kRawBytes = 8 * RAWB, kXsBytes = CPW * GS * 4, kProdBytes = 8 * GS * 4;
+    // per parity: raw window, x window (chain-major), products; then a spare slot per producer lane
+    __shared__ __align__(16) uint8_t lds[2 * (kRawBytes + kXsBytes + kProdBytes) + NP * 16];
+    auto raw_of = [&](int b) { return lds + b * (kRawBytes + kXsBytes + kProdBytes); };
+    auto xs_of = [&](int b) { return reinterpret_cast<float*>(raw_of(b) + kRawBytes); };
+    auto prod_of = [&](int b) { return reinterpret_cast<float*>(raw_of(b) + kRawBytes + kXsBytes); };
+    uint8_t* const spare = lds + 2 * (kRawBytes + kXsBytes + kProdBytes);
+
+    const int tid = threadIdx.x;
+    const bool consumer = wave_id() == 0;
+    const int row0 = blockIdx.x * Wn::kRows;
+    const float* xb = x + (size_t)blockIdx.y * n;
+
+    // Step i: producers form window i's products and stage window i+1 (from
+    // register slot r, refilled with window i+5); the consumer adds window
+    // i-1's products.  Buffers alternate by window parity.  The two roles run
+    // separate loops with the same barrier sequence, so the producers'
+    // register slots never merge with the consumer's path.
+    if (consumer) {
+        // lane: group u (row slot u / CPW, chunk slot u % CPW), chain j
+        const int j = tid & 7, u = tid >> 3, c = u % CPW;
+        const int o = row0 + u / CPW;
+        float acc = (o < out_feat && c < nchunks) ? 0.0f : -0.0f;  // -0.0: padding slot past the row's end
+        __syncthreads();
+        for (int i = 0; i <= nwin || (i & 3) != 0; i++) {
+            if (i >= 1 && i <= nwin) {
+                const float* pp = prod_of((i & 1) ^ 1) + u * GS + j * XS;
+                float4 v[8];
+#pragma unroll
+                for (int s4 = 0; s4 < 8; s4++) v[s4] = *reinterpret_cast<const float4*>(pp + 4 * s4);
+#pragma unroll
+                for (int s4 = 0; s4 < 8; s4++) {
+                    acc = acc + v[s4].x;
+                    acc = acc + v[s4].y;
+                    acc = acc + v[s4].z;
+                    acc = acc + v[s4].w;
+                }
+            }
+            __syncthreads();
+        }
+        float v = group_tree<1, 8>(acc);
+        v = group_tree<8, CPW>(v);
+        if (c == 0 && j == 0 && o < out_feat) y[(size_t)blockIdx.y * out_feat + o] = v;
+        return;
+    }
+
+    // ---- producers
+    const int pl = tid - 64;
+    const uint8_t* wlast = W + ((wbytes - 1) & ~(size_t)15);  // chunk holding the blob's last byte
+    const int last_win = (n - 1) / 256;
+    typename Wn::Chunk ch[LPL];
+#pragma unroll
+    for (int k = 0; k < LPL; k++) {
+        const int q = pl + NP * k;
+        if (q < 8 * NCH) {
+            const int g = q / NCH;
+            const int og = min(row0 + g / CPW, out_feat - 1), cg = min(g % CPW, nchunks - 1);
+            const size_t b0 = (size_t)og * row_bytes + (size_t)cg * (kChunk / 256) * WB;  // window 0 of the chunk
+            ch[k].base = W + (b0 & ~(size_t)15) + 16 * (q % NCH);
+            ch[k].cap = min(nwin - 1, last_win - cg * (kChunk / 256));
+            ch[k].step = WB;
+            ch[k].dst = g * RAWB + 16 * (q % NCH);
+        } else if (q < NLOAD) {
+            const int xi = q - 8 * NCH, s2 = xi >> 6, xl = xi & 63;
+            const int cs2 = min(s2, nchunks - 1) * kChunk;
+            ch[k].base = reinterpret_cast<const uint8_t*>(xb + cs2 + 4 * xl);
+            // x windows of the chunk, clamped so the float4 stays inside x
+            ch[k].cap = min(nwin - 1, (n - 4 - cs2 - 4 * xl) / 256);
+            ch[k].step = 1024;
+            ch[k].dst = -1 - (s2 * GS + (4 * (xl & 1)) * XS + (xl >> 1));  // x element 4*xl+i: chain 4*(xl&1)+i
+        } else {
+            ch[k].base = reinterpret_cast<const uint8_t*>(xb);
+            ch[k].cap = 0;
+            ch[k].step = 0;
+            ch[k].dst = kRawBytes + kXsBytes + kProdBytes;  // marks the spare slot
+        }
+    }
+    typename Wn::Unit un[UPL];
+#pragma unroll
+    for (int k2 = 0; k2 < UPL; k2++) {
+        const int uid = pl + NP * k2;
+        const int g = uid >> 6, j = (uid >> 3) & 7, t = uid & 7;
+        const int og = row0 + g / CPW, cg = g % CPW;
+        const size_t b0 = (size_t)min(og, out_feat - 1) * row_bytes;
+        un[k2].raw = g * RAWB + (int)(b0 & 15);  // window starts are multiples of 16 bytes apart
+        un[k2].xoff = cg * GS + j * XS + 4 * t;
+        un[k2].poff = g * GS + j * XS + 4 * t;
+        un[k2].e0 = cg * kChunk + 32 * t + j;
+        un[k2].ce = min(cg * kChunk + kChunk, n);
+        un[k2].blk = EPB == 4 ? t : 4 * t;
+        un[k2].j = j;
+        un[k2].live = og < out_feat && cg < nchunks;
+    }
+
+    auto load = [&](int w) __attribute__((always_inline)) -> typename Wn::Regs {
+        typename Wn::Regs r;
+#pragma unroll
+        for (int k = 0; k < LPL; k++) {
+            const uint8_t* a = ch[k].base + (size_t)min(w, ch[k].cap) * ch[k].step;
+            const uint4 v = *reinterpret_cast<const uint4*>(a < wlast || ch[k].step != WB ? a : wlast);
+            r[4 * k] = v.x;
+            r[4 * k + 1] = v.y;
+            r[4 * k + 2] = v.z;
+            r[4 * k + 3] = v.w;
+        }
+        return r;
+    };
+    auto stage = [&](const typename Wn::Regs& r, int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < LPL; k++) {
+            const int d = ch[k].dst;
+            if (d >= 0) {
+                uint8_t* dst = d == kRawBytes + kXsBytes + kProdBytes ? spare + 16 * pl : raw_of(b) + d;
+                *reinterpret_cast<uint4*>(dst) = make_uint4(r[4 * k], r[4 * k + 1], r[4 * k + 2], r[4 * k + 3]);
+            } else {
+                float* xd = xs_of(b) + (-1 - d);
+                xd[0] = __uint_as_float(r[4 * k]);
+                xd[XS] = __uint_as_float(r[4 * k + 1]);
+                xd[2 * XS] = __uint_as_float(r[4 * k + 2]);
+                xd[3 * XS] = __uint_as_float(r[4 * k + 3]);
+            }
+        }
+    };
+    // products of window w; every LDS read of both units is issued before any write
+    auto produce = [&](int w, int b) __attribute__((always_inline)) {
+        float wv[UPL][4];
+        float4 xv[UPL];
+#pragma unroll
+        for (int k2 = 0; k2 < UPL; k2++) {
+            const uint8_t* base = raw_of(b) + un[k2].raw;
+            if (EPB == 4) {
+                Dec::decode(base, un[k2].blk, un[k2].j, wv[k2]);  // block t: elements 32t + j + 8m
+            } else {
+#pragma unroll
+                for (int m = 0; m < 4; m++) Dec::decode(base, un[k2].blk + m, un[k2].j, &wv[k2][m]);
+            }
+            xv[k2] = *reinterpret_cast<const float4*>(xs_of(b) + un[k2].xoff);
+        }
+#pragma unroll
+        for (int k2 = 0; k2 < UPL; k2++) {
+            const float xa[4] = {xv[k2].x, xv[k2].y, xv[k2].z, xv[k2].w};
+            const int e = un[k2].e0 + w * 256;
+            const bool live = un[k2].live && w < nwin;
+            float pr[4];
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const float v = xa[m] * wv[k2][m];
+                pr[m] = (live && e + 8 * m < un[k2].ce) ? v : -0.0f;
+            }
+            *reinterpret_cast<float4*>(prod_of(b) + un[k2].poff) = make_float4(pr[0], pr[1], pr[2], pr[3]);
+        }
+    };
+    auto step = [&](int i, typename Wn::Regs& r) __attribute__((always_inline)) {
+        const int b = i & 1;
+        if (i < nwin) produce(i, b);
+        stage(r, b ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        r = load(i + 5);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+    };
+    // prologue in the loop's load order: windows 1..4 in slots 1,2,3,0
+    typename Wn::Regs r0 = load(0);
+    stage(r0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    typename Wn::Regs r1 = load(1);
+    __builtin_amdgcn_sched_barrier(0);
+    typename Wn::Regs r2 = load(2);
+    __builtin_amdgcn_sched_barrier(0);
+    typename Wn::Regs r3 = load(3);
+    __builtin_amdgcn_sched_barrier(0);
+    r0 = load(4);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    for (int i0 = 0; i0 <= nwin; i0 += 4) {
+        step(i0, r1);      // stages window i0+1 (slot 1), loads i0+5
+        step(i0 + 1, r2);  // stages i0+2, loads i0+6
+        step(i0 + 2, r3);
+        step(i0 + 3, r0);
+    }
+}
+
+template <class Dec>
+static hipError_t launch_pc(const float* x, const uint8_t* w, size_t row_bytes, float* y, int batch, int n,
+                            int out_feat, hipStream_t stream) {
+    const int nchunks = (n + kChunk - 1) / kChunk;
+    const int nwin = (min(n, kChunk) + 255) / 256;
+    const size_t wbytes = row_bytes * (size_t)out_feat;
+    int cpw = 1;
+    while (cpw < nchunks) cpw <<= 1;
+    const int rows = 8 / cpw;
+    dim3 grid((unsigned)((out_feat + rows - 1) / rows), (unsigned)batch, 1);
+#define VTQ_PC(C) hipLaunchKernelGGL((canon_pc_kernel<Dec, C>), grid, dim3(576), 0, stream, x, w, row_bytes, wbytes, y, n, out_feat, nchunks, nwin)
+    switch (cpw) {
+    case 1: VTQ_PC(1); break;
+    case 2: VTQ_PC(2); break;
+    case 4: VTQ_PC(4); break;
+    case 8: VTQ_PC(8); break;
+    default: return hipErrorInvalidValue;
+    }
+#undef VTQ_PC
+    return hipGetLastError();
+}
+
 template <class Dec>
 static hipError_t launch_dec(const float* x, const uint8_t* w, size_t row_bytes, float* y, int batch, int n,
                              int out_feat, hipStream_t stream) {
@@ -161,7 +431,17 @@ static hipError_t launch_dec(const float* x, const uint8_t* w, size_t row_bytes,
 hipError_t launch_canon_gemv(CanonFormat fmt, const float* x, const uint8_t* w, size_t row_bytes, float* y,
                              int batch, int in_feat, int out_feat, int num_cus, hipStream_t stream) {
     (void)num_cus;
-    switch (fmt) {
+    if (in_feat % 4 == 0) {  // windowed form: x rows stay float4-aligned
+        switch (fmt) {
+        case kCanonQ8_0: return launch_pc<DecQ8_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
+        case kCanonQ5_0: return launch_pc<DecQ5_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
+        case kCanonQ4_0: return launch_pc<DecQ4_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
+        case kCanonF32: return launch_pc<DecF32>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
+        case kCanonQ4KFloat: return launch_pc<DecQ4KFloat>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
+        }
+        return hipErrorInvalidValue;
+    }
+    switch (fmt) {  // per-lane form (f32 rows whose length is not a multiple of 4)
     case kCanonQ8_0: return launch_dec<DecQ8_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
     case kCanonQ5_0: return launch_dec<DecQ5_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
     case kCanonQ4_0: return launch_dec<DecQ4_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);

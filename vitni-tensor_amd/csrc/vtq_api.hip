@@ -233,7 +233,8 @@ int cached_weight(vtq_ctx* c, const uint8_t* w, size_t w_len, const uint8_t** ou
         c->weights.erase(it);
     }
     void* d = nullptr;
-    hipError_t e = hipMalloc(&d, w_len ? w_len : 16);
+    // rounded up to 16 bytes: the canonical-dot kernels fetch whole 16-byte chunks
+    hipError_t e = hipMalloc(&d, (w_len + 15) / 16 * 16 + 16);
     if (e != hipSuccess) return hip_fail(c, e, "hipMalloc(weights)");
     if (w_len) {
         e = hipMemcpy(d, w, w_len, hipMemcpyHostToDevice);

@@ -51,7 +51,8 @@ __device__ __forceinline__ float f16_hw(uint32_t h) {
 // code, and the payload-shifting formula selected for a NaN.
 __device__ __forceinline__ float f16_to_f32_sel(uint32_t h) {
     const uint32_t nan_bits = ((h & 0x8000u) << 16) | 0x7F800000u | ((h & 0x3FFu) << 13);
-    return (h & 0x7FFFu) > 0x7C00u ? __uint_as_float(nan_bits) : f16_hw(h);
+    const uint32_t m = 0u - (uint32_t)((h & 0x7FFFu) > 0x7C00u);  // all ones for a NaN
+    return __uint_as_float((__float_as_uint(f16_hw(h)) & ~m) | (nan_bits & m));
 }
 
 // Rust `(t as i32).clamp(-127, 127)` for the activation quantizer: NaN -> 0,
