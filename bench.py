@@ -8,8 +8,8 @@ them from HBM, not from the 256 MB MALL.
 
 Prints ONE JSON line (rank 0).  `value` is whole-step throughput in GB/s of
 algorithmic bytes (packed weights + fp32 x in + fp32 y out).  `roofline`
-describes the dominant kernel (q4k_gemv_kernel), timed per launch with HIP
-events on the launch stream.  `cpu_baseline` is the pinned C restatement of
+describes the dominant kernel: its average launch duration is K back-to-back
+launches bracketed by HIP events on the launch stream.  `cpu_baseline` is the pinned C restatement of
 the reference path (oracle/, the std-parallel row-parallel integer kernels)
 timed on this host's cores on the same inputs.
 
@@ -41,7 +41,7 @@ WORKLOADS = {
     "q6k_gemv_lm_head": ["q6k_32000x4096"],
     "q4k_gemm_prefill": ["q4k_gemm_14336x4096_m512"],
 }
-KERNEL_NAME = {12: "kquant_gemv_kernel<Q4K>", 14: "kquant_gemv_kernel<Q6K>", 8: "canon_gemv_kernel<DecQ8_0>"}
+KERNEL_NAME = {12: "kquant_gemv_kernel<Q4K>", 14: "kquant_gemv_kernel<Q6K>", 8: "canon_pc_kernel<DecQ8_0>"}
 INT8_MFMA_PEAK_TOPS = 5000.0
 
 
@@ -54,7 +54,24 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-rotate", action="store_true", help="reuse one weight copy (MALL-warm figure)")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="only run 20 device-to-device copies of this many MiB (HBM counter calibration)")
     return ap.parse_args()
+
+
+def calibrate_copy(mib):
+    """Plain device copies of a known size: the reference point that scales
+    rocprofv3's FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "device-to-device copy", "bytes_read": n, "bytes_written": n,
+                      "copies": 20}), flush=True)
 
 
 def cpu_baseline(cfgs, inputs, seconds):
@@ -90,6 +107,9 @@ def cpu_baseline(cfgs, inputs, seconds):
 
 def main():
     args = parse()
+    if args.calibrate_copy_mib:
+        calibrate_copy(args.calibrate_copy_mib)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the hot path shards by "
               f"output rows with no cross-device arithmetic, but multi-GPU runs are out of scope for this build.",
@@ -151,23 +171,19 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = e0.elapsed_time(e1) / args.steps
 
-    # per-launch durations of the dominant kernel (same stream, events around each launch)
-    per = [[] for _ in cfgs]
-    n_probe = min(args.steps, 100)
-    evs = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in cfgs]
-           for _ in range(n_probe)]
-    torch.cuda.synchronize()
-    for k in range(n_probe):
-        for i in range(len(cfgs)):
-            evs[k][i][0].record(stream)
+    # per-kernel average launch duration: K back-to-back launches of each
+    # config alone, bracketed by events on the launch stream (no per-launch
+    # event pairs, whose own overhead would inflate a ~10 us kernel)
+    launch_us = []
+    for i in range(len(cfgs)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for k in range(args.steps):
             launch(i, k % copies)
-            evs[k][i][1].record(stream)
-    torch.cuda.synchronize()
-    for k in range(n_probe):
-        for i in range(len(cfgs)):
-            per[i].append(evs[k][i][0].elapsed_time(evs[k][i][1]))
-    launch_us = [statistics.mean(p) * 1e3 for p in per]
-    launch_med_us = [statistics.median(p) * 1e3 for p in per]
+        b.record(stream)
+        torch.cuda.synchronize()
+        launch_us.append(a.elapsed_time(b) / args.steps * 1e3)
 
     step_bytes = sum(c.algorithmic_bytes() for c in cfgs)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
@@ -207,7 +223,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma" if gemm else "hbm",
-            "kernel": "q4k_gemm_kernel (+ act_quant_rows_kernel)" if gemm else KERNEL_NAME.get(cfgs[0].ggml_type, "?"),
+            "kernel": "q4k_gemm_kernel (+ act_quant_tiles_kernel)" if gemm else KERNEL_NAME.get(cfgs[0].ggml_type, "?"),
             "achieved": round(step_ops / len(cfgs) / (mean_launch_us * 1e-6) / 1e12, 2) if gemm else round(achieved, 2),
             "peak": INT8_MFMA_PEAK_TOPS if gemm else HBM_PEAK_GBS,
             "unit": "TOPS" if gemm else "GB/s",
@@ -215,7 +231,6 @@ def main():
             else round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
             "launch_us_mean": [round(v, 3) for v in launch_us],
-            "launch_us_median": [round(v, 3) for v in launch_med_us],
             "bytes_per_launch": [c.algorithmic_bytes() for c in cfgs],
         },
     }
