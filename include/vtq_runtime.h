@@ -1,0 +1,59 @@
+/*
+ * vtq_runtime.h -- C ABI of libvtq_runtime, the end-to-end decode driver
+ * that calls libvtq for every linear layer.
+ *
+ * It replaces the reference's quantized inference entry points:
+ *   inference::run_quantized            src/model/inference.rs:274-345
+ *   forward_quantized::step             src/model/forward_quantized.rs:288-655
+ *   GgufFile::parse / Config::from_gguf src/model/gguf.rs:305-421,
+ *                                       src/model/config.rs:156-213
+ *   QuantizedWeights::from_gguf         src/model/quant_weights.rs:121-181
+ *   blake3::hash of the GGUF blob       src/bin/vitni-receipt.rs:31
+ * with the same results bit for bit: logits of every decode step, the
+ * generated tokens and the `vitnify-receipt v2` model digest
+ * (src/cert/builder.rs:458-471).
+ *
+ * The GGUF blob is parsed once and uploaded to device memory once; every
+ * linear runs on the GPU through vtq_linear_device (include/vtq.h) on
+ * device-resident weights.  The rest of the step (embedding row, RMSNorm,
+ * RoPE, attention over the KV cache, SwiGLU, argmax) runs on the host in
+ * the reference's operation order.
+ *
+ * Status codes are those of include/vtq.h; vtqrt_last_error() gives text.
+ */
+#ifndef VTQ_RUNTIME_H
+#define VTQ_RUNTIME_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct vtqrt_model vtqrt_model;
+
+/* Parse a GGUF v2/v3 blob and upload it to HIP device `device`.  The blob is
+ * copied; the caller may free it afterwards. */
+int vtqrt_load(int device, const uint8_t *gguf, size_t len, vtqrt_model **out);
+void vtqrt_free(vtqrt_model *m);
+const char *vtqrt_last_error(const vtqrt_model *m);
+/* dim, hidden, layers, heads, kv_heads, vocab, seq_len */
+int vtqrt_dims(const vtqrt_model *m, int dims[7]);
+
+/* inference::run_quantized.  regime: VTQ_REGIME_INTEGER (std-parallel
+ * build) or VTQ_REGIME_FLOAT_FUSED (default build) for the Q4_K arm.
+ * logits (optional) receives (prompt_len + n_new) * vocab floats, one row per
+ * decode step; tokens receives the n_new generated ids; digest the v2 model
+ * digest.  weights_hash is BLAKE3 of the whole GGUF blob (vtqrt_blake3). */
+int vtqrt_run(vtqrt_model *m, int regime, const char *model_id, const uint8_t weights_hash[32],
+              const uint32_t *prompt, int prompt_len, int n_new, float *logits, uint32_t *tokens,
+              uint8_t digest[32]);
+
+/* BLAKE3-256 (crate blake3 = "1" as the reference uses it). */
+void vtqrt_blake3(const void *data, size_t len, uint8_t out[32]);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -73,6 +73,26 @@ def lib() -> ctypes.CDLL:
     L.vtqo_linear_dispatch.restype = i
     L.vtqo_matmul_f32.argtypes = [vp, vp, vp, sz, sz, sz]
     L.vtqo_matmul_f32.restype = None
+    # end-to-end decode (vtq_oracle_e2e.h)
+    for name in ("vtqo_expf", "vtqo_sinf", "vtqo_cosf", "vtqo_sqrtf"):
+        getattr(L, name).argtypes = [f]
+        getattr(L, name).restype = f
+    L.vtqo_powf.argtypes = [f, f]
+    L.vtqo_powf.restype = f
+    L.vtqo_blake3_hash.argtypes = [vp, sz, vp]
+    L.vtqo_blake3_hash.restype = None
+    L.vtqo_transcendental_hash.argtypes = [vp]
+    L.vtqo_transcendental_hash.restype = sz
+    L.vtqo_digest_v2.argtypes = [i, vp, vp, vp, i, vp, vp, vp, vp]
+    L.vtqo_digest_v2.restype = None
+    L.vtqo_model_load.argtypes = [vp, sz, ctypes.POINTER(vp), msgp]
+    L.vtqo_model_load.restype = i
+    L.vtqo_model_free.argtypes = [vp]
+    L.vtqo_model_free.restype = None
+    L.vtqo_model_dims.argtypes = [vp, vp]
+    L.vtqo_model_dims.restype = None
+    L.vtqo_run_quantized.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, i, vp, vp, vp, msgp]
+    L.vtqo_run_quantized.restype = i
     _lib = L
     return L
 
@@ -314,3 +334,87 @@ def ramp_x(n: int) -> np.ndarray:
     """Activations of the reference's tests: ((i*7919) % 1000) / 500 - 1 (src/ops/quant.rs:2023-2025)."""
     i = np.arange(n, dtype=np.int64)
     return (((i * 7919) % 1000).astype(np.float32) / np.float32(500.0)) - np.float32(1.0)
+
+
+# ---------------------------------------------------------------- end-to-end
+
+
+def expf(v: float) -> np.float32:
+    return np.float32(lib().vtqo_expf(v))
+
+
+def powf(x: float, y: float) -> np.float32:
+    return np.float32(lib().vtqo_powf(x, y))
+
+
+def sinf(v: float) -> np.float32:
+    return np.float32(lib().vtqo_sinf(v))
+
+
+def cosf(v: float) -> np.float32:
+    return np.float32(lib().vtqo_cosf(v))
+
+
+def blake3(data) -> str:
+    d = _u8(data)
+    out = (ctypes.c_uint8 * 32)()
+    lib().vtqo_blake3_hash(_ptr(d) if d.size else None, d.size, out)
+    return bytes(out).hex()
+
+
+def transcendental_hash():
+    """(input count, hex) of tests/transcendental_determinism.rs's sweep."""
+    out = (ctypes.c_uint8 * 32)()
+    n = lib().vtqo_transcendental_hash(out)
+    return int(n), bytes(out).hex()
+
+
+def _fields(items):
+    names = (ctypes.c_char_p * max(1, len(items)))(*[k.encode() for k, _ in items])
+    bufs = [bytes(v) for _, v in items]
+    datas = (ctypes.c_char_p * max(1, len(items)))(*bufs)
+    lens = (ctypes.c_size_t * max(1, len(items)))(*[len(b) for b in bufs])
+    return names, datas, lens, bufs
+
+
+def digest_v2(inputs, outputs) -> str:
+    """vitnify-receipt v2 digest of [(name, bytes)] inputs and outputs."""
+    ni, di, li, keep_i = _fields(inputs)
+    no, do, lo, keep_o = _fields(outputs)
+    out = (ctypes.c_uint8 * 32)()
+    lib().vtqo_digest_v2(len(inputs), ni, di, li, len(outputs), no, do, lo, out)
+    return bytes(out).hex()
+
+
+class Model:
+    """GGUF model for inference::run_quantized (the blob must stay alive)."""
+
+    def __init__(self, blob):
+        self.blob = _u8(blob)
+        self.handle = ctypes.c_void_p()
+        msg = ctypes.c_char_p()
+        rc = lib().vtqo_model_load(_ptr(self.blob), self.blob.size, ctypes.byref(self.handle), ctypes.byref(msg))
+        _check(rc, msg)
+        dims = np.zeros(7, dtype=np.int32)
+        lib().vtqo_model_dims(self.handle, _ptr(dims))
+        self.dim, self.hidden, self.layers, self.heads, self.kv_heads, self.vocab, self.seq_len = map(int, dims)
+
+    def run(self, prompt, n_new, weights_hash: bytes, regime=0, model_id="vitni-receipt", threads=1,
+            want_logits=True):
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        wh = np.frombuffer(bytes(weights_hash), dtype=np.uint8).copy()
+        tokens = np.zeros(max(1, n_new), dtype=np.uint32)
+        logits = np.zeros((prompt.size + n_new) * self.vocab, dtype=np.float32) if want_logits else None
+        digest = (ctypes.c_uint8 * 32)()
+        msg = ctypes.c_char_p()
+        rc = lib().vtqo_run_quantized(self.handle, regime, model_id.encode(), _ptr(wh), _ptr(prompt), prompt.size,
+                                      n_new, threads, _ptr(logits), _ptr(tokens), digest, ctypes.byref(msg))
+        _check(rc, msg)
+        if logits is not None:
+            logits = logits.reshape(prompt.size + n_new, self.vocab)
+        return tokens[:n_new], bytes(digest).hex(), logits
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            lib().vtqo_model_free(self.handle)
+            self.handle = None

@@ -1,0 +1,83 @@
+/*
+ * vtq_oracle_e2e.h -- CPU restatement of the reference's end-to-end decode
+ * path around the quantized linears (config 5).  TEST INFRASTRUCTURE ONLY:
+ * the checker for the GPU runtime, never linked into the product.
+ *
+ *  - Rust `libm = "0.2"` single-precision functions used by the forward
+ *    step (expf, powf, sinf, cosf; sqrtf is IEEE), restated from the
+ *    FreeBSD msun algorithms the crate ports.  Pinned by the reference's
+ *    PINNED_TRANSCENDENTAL hash (tests/transcendental_determinism.rs:62-63).
+ *  - BLAKE3 (crate `blake3 = "1"`), restated from the published
+ *    specification.  Pinned by the empty-input test vector and the
+ *    reference's v2 digest pin (src/cert/builder.rs:719-741).
+ *  - `vitnify-receipt v2` digest (src/cert/builder.rs:440-597).
+ *  - GGUF v2/v3 parsing (src/model/gguf.rs:305-421), Config::from_gguf
+ *    (src/model/config.rs:156-213), QuantizedWeights::from_gguf
+ *    (src/model/quant_weights.rs:121-181).
+ *  - forward_quantized::step (src/model/forward_quantized.rs:288-655) and
+ *    inference::run_quantized (src/model/inference.rs:274-345).
+ */
+#ifndef VTQ_ORACLE_E2E_H
+#define VTQ_ORACLE_E2E_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- libm (Rust libm 0.2, FreeBSD msun algorithms) ---- */
+float vtqo_expf(float x);
+float vtqo_powf(float x, float y);
+float vtqo_sinf(float x);
+float vtqo_cosf(float x);
+float vtqo_sqrtf(float x);
+
+/* ---- BLAKE3 ---- */
+typedef struct {
+    uint32_t cv[8];
+    uint64_t chunk_counter;
+    uint8_t block[64];
+    uint8_t block_len;
+    uint8_t blocks_compressed;
+    uint32_t cv_stack[54][8];
+    uint8_t cv_stack_len;
+} vtqo_blake3;
+void vtqo_blake3_init(vtqo_blake3 *h);
+void vtqo_blake3_update(vtqo_blake3 *h, const void *data, size_t len);
+void vtqo_blake3_final(const vtqo_blake3 *h, uint8_t out[32]);
+void vtqo_blake3_hash(const void *data, size_t len, uint8_t out[32]);
+
+/* BLAKE3 over every f32 result of the reference's transcendental sweep
+ * (tests/transcendental_determinism.rs:14-63). Returns the input count. */
+size_t vtqo_transcendental_hash(uint8_t out[32]);
+
+/* `vitnify-receipt v2` digest of inputs/outputs (no op/activation records):
+ * names[i] NUL-terminated, data[i]/lens[i] the field bytes. */
+void vtqo_digest_v2(int n_in, const char *const *in_names, const uint8_t *const *in_data, const size_t *in_lens,
+                    int n_out, const char *const *out_names, const uint8_t *const *out_data,
+                    const size_t *out_lens, uint8_t out[32]);
+
+/* ---- model + decode ---- */
+typedef struct vtqo_model vtqo_model;
+/* Parse a GGUF blob (borrowed; must outlive the model).  0 on success,
+ * nonzero with msg set otherwise. */
+int vtqo_model_load(const uint8_t *blob, size_t len, vtqo_model **out, const char **msg);
+void vtqo_model_free(vtqo_model *m);
+/* dim, hidden, layers, heads, kv_heads, vocab, seq_len */
+void vtqo_model_dims(const vtqo_model *m, int dims[7]);
+
+/* inference::run_quantized: regime 0 = std-parallel integer Q4_K,
+ * 1 = float-fused Q4_K.  logits (may be NULL) receives
+ * (prompt_len + n_new) * vocab floats, one row per decode step.
+ * tokens receives n_new ids; digest the v2 model digest.  weights_hash is
+ * BLAKE3 of the whole GGUF blob.  0 on success. */
+int vtqo_run_quantized(const vtqo_model *m, int regime, const char *model_id, const uint8_t weights_hash[32],
+                       const uint32_t *prompt, int prompt_len, int n_new, int threads, float *logits,
+                       uint32_t *tokens, uint8_t digest[32], const char **msg);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

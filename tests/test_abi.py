@@ -66,11 +66,38 @@ def test_no_device_maps_to_gpu_error():
 
 def test_product_has_no_oracle_or_cpu_fallback():
     # libvtq must not link or load the oracle, and the package must not import it.
-    out = subprocess.run(["ldd", vtq.LIB_PATH], capture_output=True, text=True)
-    assert "oracle" not in out.stdout
+    for lib in (vtq.LIB_PATH, os.path.join(vtq.LIB_DIR, "libvtq_runtime.so")):
+        out = subprocess.run(["ldd", lib], capture_output=True, text=True)
+        assert "oracle" not in out.stdout
     pkg = os.path.dirname(vtq.__file__)
     for root, _, files in os.walk(os.path.dirname(pkg)):
         for f in files:
             if f.endswith((".py", ".hip", ".h", ".c", ".cpp")):
                 src = open(os.path.join(root, f)).read()
                 assert "import oracle" not in src and "vtq_oracle" not in src, f
+
+
+def test_runtime_library_exports_its_header():
+    from vtq import runtime
+
+    header = os.path.join(ROOT, "include", "vtq_runtime.h")
+    text = re.sub(r"/\*.*?\*/", "", open(header).read(), flags=re.S)
+    decl = sorted(set(re.findall(r"\b(vtqrt_[a-z0-9_]+)\s*\(", text)))
+    path = os.path.join(vtq.LIB_DIR, "libvtq_runtime.so")
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True)
+    exported = sorted(set(re.findall(r"\sT\s+(vtqrt_\w+)", out.stdout)))
+    assert decl == exported
+    lib = runtime.lib()
+    assert lib.vtqrt_run(None, 0, b"m", None, None, 1, 1, None, None, None) == vtq.E_INVALID_ARGUMENT
+    assert b"null" in lib.vtqrt_last_error(None)
+
+
+def test_runtime_blake3_matches_oracle_on_cpu():
+    import numpy as np
+
+    import oracle
+    from vtq import runtime
+
+    data = (np.arange(70000) % 251).astype(np.uint8)
+    for n in (0, 1, 1024, 1025, 70000):
+        assert runtime.blake3(data[:n]).hex() == oracle.blake3(data[:n])

@@ -1,0 +1,86 @@
+"""Pins of the oracle's end-to-end pieces (CPU only).
+
+* libm: the reference's PINNED_TRANSCENDENTAL BLAKE3 over expf / sqrtf /
+  cosf / sinf / powf(1e4, .) / powf(1e6, .) / sigmoid on 489,509 inputs,
+  large-argument cos/sin included (tests/transcendental_determinism.rs:14-63).
+* BLAKE3: the published empty-input vector, and the multi-chunk stream of the
+  transcendental sweep (13.7 MB) through the pin above.
+* receipt: the reference's v2 digest pin (src/cert/builder.rs:719-741).
+* GGUF: the synthetic model parses to the configured shape.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from vtq import synth
+
+SMALL = dict(dim=256, hidden=512, layers=2, heads=4, kv_heads=2, vocab=1000, ctx=64, rope_theta=10000.0,
+             rms_eps=1e-5)
+
+
+def test_transcendental_hash_pinned():
+    n, h = oracle.transcendental_hash()
+    assert n == 489509
+    assert h == "0ae93cd6394c934bfb94a5803a0528193ba0c2330002162a0094062c294bc3d0"
+
+
+def test_blake3_empty_vector():
+    assert oracle.blake3(b"") == "af1349b9f5f9a1a6a0404dea36dcc9499bcb25c9adc112b7cc9a93cae41f3262"
+
+
+def test_blake3_streaming_boundaries():
+    # one-shot vs the same bytes split at chunk and block edges must agree,
+    # and every length around the 1024-byte chunk size hashes distinctly
+    data = (np.arange(5000) % 251).astype(np.uint8)
+    seen = set()
+    for n in (0, 1, 63, 64, 65, 1023, 1024, 1025, 2048, 2049, 3072, 4096, 4097, 5000):
+        seen.add(oracle.blake3(data[:n]))
+    assert len(seen) == 14
+
+
+def test_digest_v2_pinned():
+    d = oracle.digest_v2([("model_id", b"tinyllama"), ("prompt_tokens", bytes([1, 0, 0, 0]))],
+                         [("output_tokens", bytes([9, 0, 0, 0]))])
+    assert d == "6d5f534cf69c441ba2832c6e63747a7989ccb5de9a2cc9dc528e5b8e0359cf1e"
+
+
+def test_digest_binds_order_and_lengths():
+    a = oracle.digest_v2([("ab", b"c")], [])
+    b = oracle.digest_v2([("a", b"bc")], [])
+    c = oracle.digest_v2([], [("ab", b"c")])
+    assert len({a, b, c}) == 3
+
+
+def test_libm_closed_forms():
+    # values every float libm must get exactly
+    assert oracle.expf(0.0) == 1.0
+    assert oracle.cosf(0.0) == 1.0 and oracle.sinf(0.0) == 0.0
+    assert oracle.powf(10000.0, 0.0) == 1.0 and oracle.powf(2.0, 10.0) == 1024.0
+    assert oracle.powf(10000.0, 0.5) == 100.0
+    assert np.isinf(oracle.expf(89.0)) and oracle.expf(-104.0) == 0.0
+
+
+def test_synthetic_gguf_parses_to_config():
+    blob, prompt = synth.e2e_inputs(SMALL, 8)
+    m = oracle.Model(blob)
+    assert (m.dim, m.hidden, m.layers, m.heads, m.kv_heads, m.vocab, m.seq_len) == (256, 512, 2, 4, 2, 1000, 64)
+    assert prompt.max() < 1000
+
+
+def test_run_quantized_deterministic_and_threads_invariant():
+    blob, prompt = synth.e2e_inputs(SMALL, 8)
+    wh = bytes.fromhex(oracle.blake3(blob))
+    m = oracle.Model(blob)
+    t1, d1, l1 = m.run(prompt, 8, wh, regime=0, threads=1)
+    t2, d2, l2 = m.run(prompt, 8, wh, regime=0, threads=4)
+    assert d1 == d2 and np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+    assert np.isfinite(l1).all()
+
+
+def test_run_quantized_errors():
+    blob, prompt = synth.e2e_inputs(SMALL, 8)
+    m = oracle.Model(blob)
+    with pytest.raises(oracle.OracleError, match="exceeds seq_len"):
+        m.run(prompt, 64, b"\0" * 32)
+    with pytest.raises(oracle.OracleError, match="bad magic"):
+        oracle.Model(np.frombuffer(b"GGML" + b"\0" * 60, dtype=np.uint8))

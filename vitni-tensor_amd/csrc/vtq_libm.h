@@ -1,0 +1,486 @@
+// vtq_libm.h -- the single-precision libm functions of the reference's forward
+// step, bit-identical to the Rust crate `libm = "0.2"` it calls
+// (src/model/forward_quantized.rs:423-456 powf/cosf/sinf, :486 and
+// src/ops/rms_norm.rs:102 sqrtf, forward_quantized.rs:559, :934 expf).  The
+// crate ports FreeBSD msun (e_expf.c as restructured by musl, e_powf.c,
+// s_sinf.c / s_cosf.c, k_sinf.c, k_cosf.c, e_rem_pio2f.c, k_rem_pio2.c);
+// these are restatements of those published algorithms, usable from host
+// and device code.  Every operation is a separately rounded IEEE operation
+// (the library is compiled with -ffp-contract=off).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vtq {
+namespace libm {
+
+#define VTQ_HD __host__ __device__ __forceinline__
+
+VTQ_HD uint32_t fbits(float f) { return __builtin_bit_cast(uint32_t, f); }
+VTQ_HD float bitsf(uint32_t u) { return __builtin_bit_cast(float, u); }
+VTQ_HD double bitsd(uint64_t u) { return __builtin_bit_cast(double, u); }
+
+// x * 2^n, splitting large |n| as musl's scalbnf does
+VTQ_HD float scalbnf(float x, int n) {
+    if (n > 127) {
+        x *= 0x1p127f;
+        n -= 127;
+        if (n > 127) {
+            x *= 0x1p127f;
+            n -= 127;
+            if (n > 127) n = 127;
+        }
+    } else if (n < -126) {
+        x *= 0x1p-126f * 0x1p24f;
+        n += 126 - 24;
+        if (n < -126) {
+            x *= 0x1p-126f * 0x1p24f;
+            n += 126 - 24;
+            if (n < -126) n = -126;
+        }
+    }
+    return x * bitsf((uint32_t)(0x7f + n) << 23);
+}
+
+VTQ_HD double scalbn(double x, int n) {
+    if (n > 1023) {
+        x *= 0x1p1023;
+        n -= 1023;
+        if (n > 1023) {
+            x *= 0x1p1023;
+            n -= 1023;
+            if (n > 1023) n = 1023;
+        }
+    } else if (n < -1022) {
+        x *= 0x1p-1022 * 0x1p53;
+        n += 1022 - 53;
+        if (n < -1022) {
+            x *= 0x1p-1022 * 0x1p53;
+            n += 1022 - 53;
+            if (n < -1022) n = -1022;
+        }
+    }
+    return x * bitsd((uint64_t)(0x3ff + n) << 52);
+}
+
+// exp(x) = 2^k * exp(r), r = x - k ln2 split into hi/lo, rational form of exp(r)
+VTQ_HD float expf(float x) {
+    const float ln2hi = bitsf(0x3f317200), ln2lo = bitsf(0x35bfbe8e), invln2 = bitsf(0x3fb8aa3b);
+    const float P1 = bitsf(0x3e2aaa8f), P2 = bitsf(0xbb355215);
+    uint32_t hx = fbits(x);
+    const int sign = (int)(hx >> 31);
+    hx &= 0x7fffffff;
+    if (hx >= 0x42aeac50) {
+        if (hx > 0x7f800000) return x;
+        if (hx >= 0x42b17218 && !sign) return x * 0x1p127f;
+        if (sign && hx >= 0x42cff1b5) return 0.0f;
+    }
+    int k;
+    float hi, lo;
+    if (hx > 0x3eb17218) {
+        if (hx > 0x3f851592)
+            k = (int)(invln2 * x + (sign ? -0.5f : 0.5f));
+        else
+            k = 1 - sign - sign;
+        const float kf = (float)k;
+        hi = x - kf * ln2hi;
+        lo = kf * ln2lo;
+        x = hi - lo;
+    } else if (hx > 0x39000000) {
+        k = 0;
+        hi = x;
+        lo = 0.0f;
+    } else {
+        return 1.0f + x;
+    }
+    const float xx = x * x;
+    const float c = x - xx * (P1 + xx * P2);
+    const float y = 1.0f + (x * c / (2.0f - c) - lo + hi);
+    return k == 0 ? y : scalbnf(y, k);
+}
+
+VTQ_HD float sqrtf(float x) { return __builtin_sqrtf(x); }  // IEEE, correctly rounded
+
+VTQ_HD float fabsf_(float x) { return bitsf(fbits(x) & 0x7fffffffu); }
+
+// x^y = 2^(y * log2 x): log2|x| carried as 12-bit head + tail, the product
+// split the same way, then 2^z by a rational approximation
+VTQ_HD float powf(float x, float y) {
+    const float bp[2] = {1.0f, 1.5f};
+    const float dp_h[2] = {0.0f, bitsf(0x3f15c000)};
+    const float dp_l[2] = {0.0f, bitsf(0x35d1cfdc)};
+    const float two24 = bitsf(0x4b800000), huge = 1.0e30f, tiny = 1.0e-30f;
+    const float L1 = bitsf(0x3f19999a), L2 = bitsf(0x3edb6db7), L3 = bitsf(0x3eaaaaab), L4 = bitsf(0x3e8ba305),
+                L5 = bitsf(0x3e6c3255), L6 = bitsf(0x3e53f142);
+    const float P1 = bitsf(0x3e2aaaab), P2 = bitsf(0xbb360b61), P3 = bitsf(0x388ab355), P4 = bitsf(0xb5ddea0e),
+                P5 = bitsf(0x3331bb4c);
+    const float lg2 = bitsf(0x3f317218), lg2_h = bitsf(0x3f317200), lg2_l = bitsf(0x35bfbe8c);
+    const float ovt = 4.2995665694e-08f;
+    const float cp = bitsf(0x3f76384f), cp_h = bitsf(0x3f764000), cp_l = bitsf(0xb8f623c6);
+    const float ivln2 = bitsf(0x3fb8aa3b), ivln2_h = bitsf(0x3fb8aa00), ivln2_l = bitsf(0x36eca570);
+
+    float z, ax, z_h, z_l, p_h, p_l, y1, t1, t2, r, s, sn, t, u, v, w;
+    int32_t i, j, k, yisint, n;
+    const int32_t hx = (int32_t)fbits(x), hy = (int32_t)fbits(y);
+    int32_t ix = hx & 0x7fffffff;
+    const int32_t iy = hy & 0x7fffffff;
+
+    if (iy == 0) return 1.0f;
+    if (hx == 0x3f800000) return 1.0f;
+    if (ix > 0x7f800000 || iy > 0x7f800000) return x + y;
+    yisint = 0;
+    if (hx < 0) {
+        if (iy >= 0x4b800000) {
+            yisint = 2;
+        } else if (iy >= 0x3f800000) {
+            k = (iy >> 23) - 0x7f;
+            j = iy >> (23 - k);
+            if ((j << (23 - k)) == iy) yisint = 2 - (j & 1);
+        }
+    }
+    if (iy == 0x7f800000) {
+        if (ix == 0x3f800000) return 1.0f;
+        if (ix > 0x3f800000) return hy >= 0 ? y : 0.0f;
+        return hy >= 0 ? 0.0f : -y;
+    }
+    if (iy == 0x3f800000) return hy >= 0 ? x : 1.0f / x;
+    if (hy == 0x40000000) return x * x;
+    if (hy == 0x3f000000 && hx >= 0) return sqrtf(x);
+
+    ax = fabsf_(x);
+    if (ix == 0x7f800000 || ix == 0 || ix == 0x3f800000) {
+        z = ax;
+        if (hy < 0) z = 1.0f / z;
+        if (hx < 0) {
+            if (((ix - 0x3f800000) | yisint) == 0)
+                z = (z - z) / (z - z);
+            else if (yisint == 1)
+                z = -z;
+        }
+        return z;
+    }
+    sn = 1.0f;
+    if (hx < 0) {
+        if (yisint == 0) return (x - x) / (x - x);
+        if (yisint == 1) sn = -1.0f;
+    }
+    if (iy > 0x4d000000) {
+        if (ix < 0x3f7ffff8) return hy < 0 ? sn * huge * huge : sn * tiny * tiny;
+        if (ix > 0x3f800007) return hy > 0 ? sn * huge * huge : sn * tiny * tiny;
+        t = ax - 1.0f;
+        w = (t * t) * (0.5f - t * (0.333333333333f - t * 0.25f));
+        u = ivln2_h * t;
+        v = t * ivln2_l - w * ivln2;
+        t1 = u + v;
+        t1 = bitsf(fbits(t1) & 0xfffff000u);
+        t2 = v - (t1 - u);
+    } else {
+        float s2, s_h, s_l, t_h, t_l;
+        n = 0;
+        if (ix < 0x00800000) {
+            ax *= two24;
+            n -= 24;
+            ix = (int32_t)fbits(ax);
+        }
+        n += (ix >> 23) - 0x7f;
+        j = ix & 0x007fffff;
+        ix = j | 0x3f800000;
+        if (j <= 0x1cc471) {
+            k = 0;
+        } else if (j < 0x5db3d7) {
+            k = 1;
+        } else {
+            k = 0;
+            n += 1;
+            ix -= 0x00800000;
+        }
+        ax = bitsf((uint32_t)ix);
+        u = ax - bp[k];
+        v = 1.0f / (ax + bp[k]);
+        s = u * v;
+        s_h = bitsf(fbits(s) & 0xfffff000u);
+        const uint32_t is = (((uint32_t)ix >> 1) & 0xfffff000u) | 0x20000000u;
+        t_h = bitsf(is + 0x00400000u + ((uint32_t)k << 21));
+        t_l = ax - (t_h - bp[k]);
+        s_l = v * ((u - s_h * t_h) - s_h * t_l);
+        s2 = s * s;
+        r = s2 * s2 * (L1 + s2 * (L2 + s2 * (L3 + s2 * (L4 + s2 * (L5 + s2 * L6)))));
+        r += s_l * (s_h + s);
+        s2 = s_h * s_h;
+        t_h = 3.0f + s2 + r;
+        t_h = bitsf(fbits(t_h) & 0xfffff000u);
+        t_l = r - ((t_h - 3.0f) - s2);
+        u = s_h * t_h;
+        v = s_l * t_h + t_l * s;
+        p_h = u + v;
+        p_h = bitsf(fbits(p_h) & 0xfffff000u);
+        p_l = v - (p_h - u);
+        z_h = cp_h * p_h;
+        z_l = cp_l * p_h + p_l * cp + dp_l[k];
+        t = (float)n;
+        t1 = ((z_h + z_l) + dp_h[k]) + t;
+        t1 = bitsf(fbits(t1) & 0xfffff000u);
+        t2 = z_l - (((t1 - t) - dp_h[k]) - z_h);
+    }
+    y1 = bitsf(fbits(y) & 0xfffff000u);
+    p_l = (y - y1) * t1 + y * t2;
+    p_h = y1 * t1;
+    z = p_l + p_h;
+    j = (int32_t)fbits(z);
+    if (j > 0x43000000) {
+        return sn * huge * huge;
+    } else if (j == 0x43000000) {
+        if (p_l + ovt > z - p_h) return sn * huge * huge;
+    } else if ((j & 0x7fffffff) > 0x43160000) {
+        return sn * tiny * tiny;
+    } else if ((uint32_t)j == 0xc3160000u && p_l <= z - p_h) {
+        return sn * tiny * tiny;
+    }
+    i = j & 0x7fffffff;
+    k = (i >> 23) - 0x7f;
+    n = 0;
+    if (i > 0x3f000000) {
+        n = j + (0x00800000 >> (k + 1));
+        k = ((n & 0x7fffffff) >> 23) - 0x7f;
+        t = bitsf((uint32_t)n & ~(0x007fffffu >> k));
+        n = ((n & 0x007fffff) | 0x00800000) >> (23 - k);
+        if (j < 0) n = -n;
+        p_h -= t;
+    }
+    t = p_l + p_h;
+    t = bitsf(fbits(t) & 0xffff8000u);
+    u = t * lg2_h;
+    v = (p_l - (t - p_h)) * lg2 + t * lg2_l;
+    z = u + v;
+    w = v - (z - u);
+    t = z * z;
+    t1 = z - t * (P1 + t * (P2 + t * (P3 + t * (P4 + t * P5))));
+    r = (z * t1) / (t1 - 2.0f) - (w + z * w);
+    z = 1.0f - (r - z);
+    j = (int32_t)fbits(z);
+    j += (int32_t)((uint32_t)n << 23);
+    if ((j >> 23) <= 0)
+        z = scalbnf(z, n);
+    else
+        z = bitsf((uint32_t)j);
+    return sn * z;
+}
+
+// minimax kernels of sin and cos on [-pi/4, pi/4], evaluated in double
+VTQ_HD float sindf(double x) {
+    const double S1 = bitsd(0xbfc5555554cbac77ull), S2 = bitsd(0x3f811110896efbb2ull),
+                 S3 = bitsd(0xbf2a00f9e2cae774ull), S4 = bitsd(0x3ec6cd878c3b46a7ull);
+    const double z = x * x, w = z * z, r = S3 + z * S4, s = z * x;
+    return (float)((x + s * (S1 + z * S2)) + s * w * r);
+}
+VTQ_HD float cosdf(double x) {
+    const double C0 = bitsd(0xbfdffffffd0c5e81ull), C1 = bitsd(0x3fa55553e1053a42ull),
+                 C2 = bitsd(0xbf56c087e80f1e27ull), C3 = bitsd(0x3ef99342e0ee5069ull);
+    const double z = x * x, w = z * z, r = C2 + z * C3;
+    return (float)(((1.0 + z * C0) + w * C1) + (w * z) * r);
+}
+
+// 2/pi in 24-bit chunks: enough for every float argument
+__host__ __device__ inline int32_t two_over_pi(int i) {
+    constexpr int32_t t[] = {0xA2F983, 0x6E4E44, 0x1529FC, 0x2757D1, 0xF534DD, 0xC0DB62, 0x95993C, 0x439041,
+                             0xFE5163, 0xABDEBB, 0xC561B7, 0x246E3A, 0x424DD2, 0xE00649, 0x2EEA09, 0xD1921C,
+                             0xFE1DEB, 0x1CB129, 0xA73EE8, 0x8235F5, 0x2EBB44, 0x84E99C, 0x7026B4, 0x5F7E41};
+    return t[i];
+}
+
+// Payne-Hanek reduction of one 24-bit input word with a 24-bit result
+// (the single-precision case of k_rem_pio2.c)
+__host__ __device__ inline int rem_pio2_large(double x0, double* y, int e0) {
+    const int jk = 3, jp = 3;
+    const double PIo2[4] = {bitsd(0x3FF921FB40000000ull), bitsd(0x3E74442D00000000ull),
+                            bitsd(0x3CF8469880000000ull), bitsd(0x3B78CC5160000000ull)};
+    int32_t jz, jv, carry, n, iq[20], i, j, k, q0, ih;
+    double z, fw, f[20], fq[20], q[20];
+    jv = (e0 - 3) / 24;
+    if (jv < 0) jv = 0;
+    q0 = e0 - 24 * (jv + 1);
+    for (i = 0, j = jv; i <= jk; i++, j++) f[i] = j < 0 ? 0.0 : (double)two_over_pi(j);
+    for (i = 0; i <= jk; i++) q[i] = 0.0 + x0 * f[i];
+    jz = jk;
+    for (;;) {
+        for (i = 0, j = jz, z = q[jz]; j > 0; i++, j--) {
+            fw = (double)(int32_t)(0x1p-24 * z);
+            iq[i] = (int32_t)(z - 0x1p24 * fw);
+            z = q[j - 1] + fw;
+        }
+        z = scalbn(z, q0);
+        z -= 8.0 * __builtin_floor(z * 0.125);
+        n = (int32_t)z;
+        z -= (double)n;
+        ih = 0;
+        if (q0 > 0) {
+            i = iq[jz - 1] >> (24 - q0);
+            n += i;
+            iq[jz - 1] -= i << (24 - q0);
+            ih = iq[jz - 1] >> (23 - q0);
+        } else if (q0 == 0) {
+            ih = iq[jz - 1] >> 23;
+        } else if (z >= 0.5) {
+            ih = 2;
+        }
+        if (ih > 0) {
+            n += 1;
+            carry = 0;
+            for (i = 0; i < jz; i++) {
+                j = iq[i];
+                if (carry == 0) {
+                    if (j != 0) {
+                        carry = 1;
+                        iq[i] = 0x1000000 - j;
+                    }
+                } else {
+                    iq[i] = 0xffffff - j;
+                }
+            }
+            if (q0 == 1) iq[jz - 1] &= 0x7fffff;
+            if (q0 == 2) iq[jz - 1] &= 0x3fffff;
+            if (ih == 2) {
+                z = 1.0 - z;
+                if (carry != 0) z -= scalbn(1.0, q0);
+            }
+        }
+        if (z == 0) {
+            j = 0;
+            for (i = jz - 1; i >= jk; i--) j |= iq[i];
+            if (j == 0) {  // need more terms of 2/pi
+                for (k = 1; iq[jk - k] == 0; k++) {
+                }
+                for (i = jz + 1; i <= jz + k; i++) {
+                    f[i] = (double)two_over_pi(jv + i);
+                    q[i] = 0.0 + x0 * f[i];
+                }
+                jz += k;
+                continue;
+            }
+        }
+        break;
+    }
+    if (z == 0.0) {
+        jz -= 1;
+        q0 -= 24;
+        while (iq[jz] == 0) {
+            jz--;
+            q0 -= 24;
+        }
+    } else {
+        z = scalbn(z, -q0);
+        if (z >= 0x1p24) {
+            fw = (double)(int32_t)(0x1p-24 * z);
+            iq[jz] = (int32_t)(z - 0x1p24 * fw);
+            jz += 1;
+            q0 += 24;
+            iq[jz] = (int32_t)fw;
+        } else {
+            iq[jz] = (int32_t)z;
+        }
+    }
+    fw = scalbn(1.0, q0);
+    for (i = jz; i >= 0; i--) {
+        q[i] = fw * (double)iq[i];
+        fw *= 0x1p-24;
+    }
+    for (i = jz; i >= 0; i--) {
+        for (fw = 0.0, k = 0; k <= jp && k <= jz - i; k++) fw += PIo2[k] * q[i + k];
+        fq[jz - i] = fw;
+    }
+    fw = 0.0;
+    for (i = jz; i >= 0; i--) fw += fq[i];
+    *y = ih == 0 ? fw : -fw;
+    return n & 7;
+}
+
+// x = n*pi/2 + y, |y| <~ pi/4
+VTQ_HD int rem_pio2f(float x, double* y) {
+    const double toint = 1.5 / 2.22044604925031308085e-16;
+    const double invpio2 = bitsd(0x3FE45F306DC9C883ull), pio2_1 = bitsd(0x3FF921FB50000000ull),
+                 pio2_1t = bitsd(0x3E5110B4611A6263ull);
+    const uint32_t ix = fbits(x) & 0x7fffffff;
+    if (ix < 0x4dc90fdb) {
+        const double fn = (double)x * invpio2 + toint - toint;
+        *y = (double)x - fn * pio2_1 - fn * pio2_1t;
+        return (int32_t)fn;
+    }
+    if (ix >= 0x7f800000) {
+        *y = (double)(x - x);
+        return 0;
+    }
+    const int e0 = (int)(ix >> 23) - (0x7f + 23);
+    double ty;
+    const int n = rem_pio2_large((double)bitsf(ix - ((uint32_t)e0 << 23)), &ty, e0);
+    if (fbits(x) >> 31) {
+        *y = -ty;
+        return -n;
+    }
+    *y = ty;
+    return n;
+}
+
+VTQ_HD float sinf(float x) {
+    const double s1 = bitsd(0x3FF921FB54442D18ull), s2 = bitsd(0x400921FB54442D18ull),
+                 s3 = bitsd(0x4012D97C7F3321D2ull), s4 = bitsd(0x401921FB54442D18ull);
+    const double xd = (double)x;
+    uint32_t ix = fbits(x);
+    const bool sign = (ix >> 31) != 0;
+    ix &= 0x7fffffff;
+    if (ix <= 0x3f490fda) {
+        if (ix < 0x39800000) return x;
+        return sindf(xd);
+    }
+    if (ix <= 0x407b53d1) {
+        if (ix <= 0x4016cbe3) return sign ? -cosdf(xd + s1) : cosdf(xd - s1);
+        return sindf(sign ? -(xd + s2) : -(xd - s2));
+    }
+    if (ix <= 0x40e231d5) {
+        if (ix <= 0x40afeddf) return sign ? cosdf(xd + s3) : -cosdf(xd - s3);
+        return sindf(sign ? xd + s4 : xd - s4);
+    }
+    if (ix >= 0x7f800000) return x - x;
+    double y;
+    const int n = rem_pio2f(x, &y);
+    switch (n & 3) {
+    case 0: return sindf(y);
+    case 1: return cosdf(y);
+    case 2: return sindf(-y);
+    default: return -cosdf(y);
+    }
+}
+
+VTQ_HD float cosf(float x) {
+    const double c1 = bitsd(0x3FF921FB54442D18ull), c2 = bitsd(0x400921FB54442D18ull),
+                 c3 = bitsd(0x4012D97C7F3321D2ull), c4 = bitsd(0x401921FB54442D18ull);
+    const double xd = (double)x;
+    uint32_t ix = fbits(x);
+    const bool sign = (ix >> 31) != 0;
+    ix &= 0x7fffffff;
+    if (ix <= 0x3f490fda) {
+        if (ix < 0x39800000) return 1.0f;
+        return cosdf(xd);
+    }
+    if (ix <= 0x407b53d1) {
+        if (ix > 0x4016cbe3) return -cosdf(sign ? xd + c2 : xd - c2);
+        return sign ? sindf(xd + c1) : sindf(c1 - xd);
+    }
+    if (ix <= 0x40e231d5) {
+        if (ix > 0x40afeddf) return cosdf(sign ? xd + c4 : xd - c4);
+        return sign ? sindf(-xd - c3) : sindf(xd - c3);
+    }
+    if (ix >= 0x7f800000) return x - x;
+    double y;
+    const int n = rem_pio2f(x, &y);
+    switch (n & 3) {
+    case 0: return cosdf(y);
+    case 1: return sindf(-y);
+    case 2: return -cosdf(y);
+    default: return sindf(y);
+    }
+}
+
+#undef VTQ_HD
+}  // namespace libm
+}  // namespace vtq

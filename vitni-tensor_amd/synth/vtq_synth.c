@@ -6,6 +6,10 @@
  */
 #include "vtq_synth.h"
 
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
 #include <math.h>
 #include <string.h>
 
@@ -158,4 +162,144 @@ void vtqs_q4_0(uint64_t seed, uint8_t *w, size_t rows, size_t in_feat, float sig
             blk[2 + e / 2] |= (uint8_t)((e & 1) ? q << 4 : q);
         }
     }
+}
+
+void vtqs_tokens(uint64_t seed, uint32_t *out, size_t n, uint32_t vocab) {
+    uint64_t s = seed;
+    for (size_t i = 0; i < n; i++) out[i] = uni(&s, vocab);
+}
+
+/* ---- GGUF v3 writer ---- */
+typedef struct {
+    uint8_t *out;
+    size_t pos;
+} gw_t;
+
+static void gw_bytes(gw_t *g, const void *p, size_t n) {
+    if (g->out) memcpy(g->out + g->pos, p, n);
+    g->pos += n;
+}
+static void gw_u32(gw_t *g, uint32_t v) {
+    uint8_t b[4] = {(uint8_t)v, (uint8_t)(v >> 8), (uint8_t)(v >> 16), (uint8_t)(v >> 24)};
+    gw_bytes(g, b, 4);
+}
+static void gw_u64(gw_t *g, uint64_t v) {
+    gw_u32(g, (uint32_t)v);
+    gw_u32(g, (uint32_t)(v >> 32));
+}
+static void gw_str(gw_t *g, const char *s) {
+    gw_u64(g, strlen(s));
+    gw_bytes(g, s, strlen(s));
+}
+static void gw_kv_u32(gw_t *g, const char *k, uint32_t v) {
+    gw_str(g, k);
+    gw_u32(g, 4);
+    gw_u32(g, v);
+}
+static void gw_kv_f32(gw_t *g, const char *k, float v) {
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    gw_str(g, k);
+    gw_u32(g, 6);
+    gw_u32(g, b);
+}
+
+typedef struct {
+    char name[64];
+    uint32_t type;           /* 0 F32, 12 Q4_K, 14 Q6_K */
+    uint64_t ne0, ne1;       /* row length, rows (ne1 = 0: 1-D) */
+    size_t nbytes, offset;
+} gt_t;
+
+static size_t gt_bytes(const gt_t *t) {
+    const uint64_t rows = t->ne1 ? t->ne1 : 1;
+    switch (t->type) {
+    case 12: return (size_t)(rows * (t->ne0 / 256) * 144);
+    case 14: return (size_t)(rows * (t->ne0 / 256) * 210);
+    default: return (size_t)(rows * t->ne0 * 4);
+    }
+}
+
+size_t vtqs_llama_gguf(const vtqs_llama *c, uint64_t seed, uint8_t *out) {
+    const uint32_t head = c->dim / c->heads, kv_dim = c->kv_heads * head;
+    const size_t nt = 3 + 9 * (size_t)c->layers;
+    gt_t *ts = (gt_t *)calloc(nt, sizeof(gt_t));
+    size_t k = 0;
+#define T(NAME, TYPE, NE0, NE1)                                              \
+    do {                                                                     \
+        snprintf(ts[k].name, sizeof ts[k].name, "%s", NAME);                 \
+        ts[k].type = TYPE;                                                   \
+        ts[k].ne0 = NE0;                                                     \
+        ts[k].ne1 = NE1;                                                     \
+        k++;                                                                 \
+    } while (0)
+    T("token_embd.weight", 12, c->dim, c->vocab);
+    for (uint32_t l = 0; l < c->layers; l++) {
+        char nm[64];
+        snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l); T(nm, 0, c->dim, 0);
+        snprintf(nm, sizeof nm, "blk.%u.attn_q.weight", l); T(nm, 12, c->dim, c->dim);
+        snprintf(nm, sizeof nm, "blk.%u.attn_k.weight", l); T(nm, 12, c->dim, kv_dim);
+        snprintf(nm, sizeof nm, "blk.%u.attn_v.weight", l); T(nm, 12, c->dim, kv_dim);
+        snprintf(nm, sizeof nm, "blk.%u.attn_output.weight", l); T(nm, 12, c->dim, c->dim);
+        snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l); T(nm, 0, c->dim, 0);
+        snprintf(nm, sizeof nm, "blk.%u.ffn_gate.weight", l); T(nm, 12, c->dim, c->hidden);
+        snprintf(nm, sizeof nm, "blk.%u.ffn_up.weight", l); T(nm, 12, c->dim, c->hidden);
+        snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l); T(nm, 12, c->hidden, c->dim);
+    }
+    T("output_norm.weight", 0, c->dim, 0);
+    T("output.weight", 14, c->dim, c->vocab);
+#undef T
+    size_t off = 0;
+    for (size_t i = 0; i < nt; i++) {
+        ts[i].nbytes = gt_bytes(&ts[i]);
+        ts[i].offset = off;
+        off += (ts[i].nbytes + 31) / 32 * 32;
+    }
+    gw_t g = {out, 0};
+    gw_bytes(&g, "GGUF", 4);
+    gw_u32(&g, 3);
+    gw_u64(&g, nt);
+    gw_u64(&g, 11);
+    gw_str(&g, "general.architecture");
+    gw_u32(&g, 8);
+    gw_str(&g, "llama");
+    gw_kv_u32(&g, "general.alignment", 32);
+    gw_kv_u32(&g, "llama.embedding_length", c->dim);
+    gw_kv_u32(&g, "llama.feed_forward_length", c->hidden);
+    gw_kv_u32(&g, "llama.block_count", c->layers);
+    gw_kv_u32(&g, "llama.attention.head_count", c->heads);
+    gw_kv_u32(&g, "llama.attention.head_count_kv", c->kv_heads);
+    gw_kv_u32(&g, "llama.context_length", c->ctx);
+    gw_kv_u32(&g, "llama.vocab_size", c->vocab);
+    gw_kv_f32(&g, "llama.rope.freq_base", c->rope_theta);
+    gw_kv_f32(&g, "llama.attention.layer_norm_rms_epsilon", c->rms_eps);
+    for (size_t i = 0; i < nt; i++) {
+        gw_str(&g, ts[i].name);
+        gw_u32(&g, ts[i].ne1 ? 2 : 1);
+        gw_u64(&g, ts[i].ne0);
+        if (ts[i].ne1) gw_u64(&g, ts[i].ne1);
+        gw_u32(&g, ts[i].type);
+        gw_u64(&g, ts[i].offset);
+    }
+    const size_t base = (g.pos + 31) / 32 * 32;
+    if (out) memset(out + g.pos, 0, base - g.pos);
+    if (out) {
+        for (size_t i = 0; i < nt; i++) {
+            uint8_t *p = out + base + ts[i].offset;
+            const uint64_t ts_seed = seed + i;
+            const size_t pad = (ts[i].nbytes + 31) / 32 * 32 - ts[i].nbytes;
+            if (ts[i].type == 12) {
+                vtqs_q4_k(ts_seed, p, ts[i].ne1, ts[i].ne0, 0.01f);
+            } else if (ts[i].type == 14) {
+                vtqs_q6_k(ts_seed, p, ts[i].ne1, ts[i].ne0, 0.01f);
+            } else {
+                float *f = (float *)p;
+                vtqs_normal_f32(ts_seed, f, ts[i].ne0, 0.05f);
+                for (uint64_t e = 0; e < ts[i].ne0; e++) f[e] = 1.0f + f[e];
+            }
+            memset(p + ts[i].nbytes, 0, pad);
+        }
+    }
+    free(ts);
+    return base + off;
 }

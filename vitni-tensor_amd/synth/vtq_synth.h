@@ -32,6 +32,31 @@ void vtqs_q5_0(uint64_t seed, uint8_t *w, size_t rows, size_t in_feat, float sig
 void vtqs_q4_0(uint64_t seed, uint8_t *w, size_t rows, size_t in_feat, float sigma);
 void vtqs_bytes(uint64_t seed, uint8_t *w, size_t n);
 
+/* Token ids U[0, vocab). */
+void vtqs_tokens(uint64_t seed, uint32_t *out, size_t n, uint32_t vocab);
+
+/* A random-init Llama model as a GGUF v3 blob (the file format the
+ * reference loads, src/model/gguf.rs:305-421): general.architecture
+ * "llama", the llama.* hyper-parameters (u32; rope.freq_base and
+ * attention.layer_norm_rms_epsilon f32), general.alignment 32, and tensors
+ *   token_embd.weight            Q4_K [dim, vocab]
+ *   blk.L.attn_norm.weight       F32  [dim]        1 + N(0, 0.05)
+ *   blk.L.attn_q/attn_output     Q4_K [dim, dim]
+ *   blk.L.attn_k/attn_v          Q4_K [dim, kv_dim]
+ *   blk.L.ffn_norm.weight        F32  [dim]
+ *   blk.L.ffn_gate/ffn_up        Q4_K [dim, hidden]
+ *   blk.L.ffn_down               Q4_K [hidden, dim]
+ *   output_norm.weight           F32  [dim]
+ *   output.weight                Q6_K [dim, vocab]
+ * (GGML order: the first dimension is the row length).  Blocks come from
+ * the generators above with sigma 0.01; tensor i uses seed + i.  Returns
+ * the blob size; writes it to out when out is not NULL. */
+typedef struct {
+    uint32_t dim, hidden, layers, heads, kv_heads, vocab, ctx;
+    float rope_theta, rms_eps;
+} vtqs_llama;
+size_t vtqs_llama_gguf(const vtqs_llama *cfg, uint64_t seed, uint8_t *out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,86 @@
+"""ctypes bindings of libvtq_runtime (include/vtq_runtime.h): the reference's
+quantized decode (inference::run_quantized) with every linear on the GPU."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from . import LIB_DIR, load_library, GpuError, Internal, InvalidArgument, NotImplementedDtype
+
+_rt = None
+_ERR = {1: Internal, 2: GpuError, 3: NotImplementedDtype, 4: InvalidArgument}
+
+
+def lib() -> ctypes.CDLL:
+    global _rt
+    if _rt is None:
+        load_library()  # torch first, then libvtq: one HIP runtime per process
+        path = os.path.join(LIB_DIR, "libvtq_runtime.so")
+        if not os.path.exists(path):
+            raise ImportError(f"{path} is missing (run __graft_entry__.build())")
+        L = ctypes.CDLL(path)
+        vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        L.vtqrt_load.argtypes = [i, vp, sz, ctypes.POINTER(vp)]
+        L.vtqrt_load.restype = i
+        L.vtqrt_free.argtypes = [vp]
+        L.vtqrt_free.restype = None
+        L.vtqrt_last_error.argtypes = [vp]
+        L.vtqrt_last_error.restype = ctypes.c_char_p
+        L.vtqrt_dims.argtypes = [vp, vp]
+        L.vtqrt_dims.restype = i
+        L.vtqrt_run.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, vp, vp, vp]
+        L.vtqrt_run.restype = i
+        L.vtqrt_blake3.argtypes = [vp, sz, vp]
+        L.vtqrt_blake3.restype = None
+        _rt = L
+    return _rt
+
+
+def blake3(data) -> bytes:
+    d = np.ascontiguousarray(np.frombuffer(bytes(data), dtype=np.uint8) if isinstance(data, (bytes, bytearray))
+                             else data, dtype=np.uint8)
+    out = (ctypes.c_uint8 * 32)()
+    lib().vtqrt_blake3(d.ctypes.data if d.size else None, d.size, out)
+    return bytes(out)
+
+
+class Model:
+    """A GGUF model uploaded to one GPU (vtqrt_load)."""
+
+    def __init__(self, blob, device: int = 0):
+        b = np.ascontiguousarray(blob, dtype=np.uint8)
+        self.handle = ctypes.c_void_p()
+        rc = lib().vtqrt_load(device, b.ctypes.data, b.size, ctypes.byref(self.handle))
+        if rc:
+            msg = lib().vtqrt_last_error(self.handle).decode()
+            lib().vtqrt_free(self.handle)
+            self.handle = None
+            raise _ERR.get(rc, GpuError)(msg)
+        dims = np.zeros(7, dtype=np.int32)
+        lib().vtqrt_dims(self.handle, dims.ctypes.data)
+        self.dim, self.hidden, self.layers, self.heads, self.kv_heads, self.vocab, self.seq_len = map(int, dims)
+
+    def run(self, prompt, n_new, weights_hash: bytes, regime=0, model_id="vitni-receipt", want_logits=True):
+        """(generated tokens, v2 digest hex, logits [steps][vocab] or None)."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        wh = np.frombuffer(bytes(weights_hash), dtype=np.uint8).copy()
+        tokens = np.zeros(max(1, n_new), dtype=np.uint32)
+        logits = np.zeros((prompt.size + n_new) * self.vocab, dtype=np.float32) if want_logits else None
+        digest = (ctypes.c_uint8 * 32)()
+        rc = lib().vtqrt_run(self.handle, regime, model_id.encode(), wh.ctypes.data, prompt.ctypes.data, prompt.size,
+                             n_new, None if logits is None else logits.ctypes.data, tokens.ctypes.data, digest)
+        if rc:
+            raise _ERR.get(rc, GpuError)(lib().vtqrt_last_error(self.handle).decode())
+        if logits is not None:
+            logits = logits.reshape(prompt.size + n_new, self.vocab)
+        return tokens[:n_new], bytes(digest).hex(), logits
+
+    def close(self):
+        if self.handle:
+            lib().vtqrt_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()

@@ -21,6 +21,14 @@ SCALE_SIGMA = 0.01  # d, dmin = f16(|N(0, 0.01)|)
 _synth = None
 
 
+class LlamaCfg(ctypes.Structure):
+    """vtqs_llama (synth/vtq_synth.h)"""
+
+    _fields_ = [("dim", ctypes.c_uint32), ("hidden", ctypes.c_uint32), ("layers", ctypes.c_uint32),
+                ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32), ("vocab", ctypes.c_uint32),
+                ("ctx", ctypes.c_uint32), ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+
 def lib() -> ctypes.CDLL:
     global _synth
     if _synth is None:
@@ -38,6 +46,10 @@ def lib() -> ctypes.CDLL:
         s.vtqs_bytes.restype = None
         s.vtqs_f32_to_f16_rne.argtypes = [f]
         s.vtqs_f32_to_f16_rne.restype = ctypes.c_uint16
+        s.vtqs_tokens.argtypes = [u64, vp, sz, ctypes.c_uint32]
+        s.vtqs_tokens.restype = None
+        s.vtqs_llama_gguf.argtypes = [ctypes.POINTER(LlamaCfg), u64, vp]
+        s.vtqs_llama_gguf.restype = sz
         _synth = s
     return _synth
 
@@ -112,3 +124,37 @@ CONFIGS = {
     "q6k_32000x4096": Config(3, "q6k_32000x4096", Q6_K, 32000, 4096, 1),
     "q4k_gemm_14336x4096_m512": Config(4, "q4k_gemm_14336x4096_m512", Q4_K, 14336, 4096, 512),
 }
+
+
+# ---------------------------------------------------------------- config 5
+
+# random-init Llama 1.1B, Q4_K attention/FFN and
+# token_embd, Q6_K output head, F32 norms; 128 random prompt ids, 64 new tokens
+LLAMA_1B1 = dict(dim=2048, hidden=5632, layers=22, heads=32, kv_heads=4, vocab=32000, ctx=1024,
+                 rope_theta=10000.0, rms_eps=1e-5)
+E2E_INDEX = 4
+E2E_PROMPT = 128
+E2E_NEW = 64
+
+
+def llama_gguf(cfg: dict, seed: int) -> np.ndarray:
+    """GGUF v3 blob of a random-init Llama model (synth/vtq_synth.h)."""
+    c = LlamaCfg(**cfg)
+    n = lib().vtqs_llama_gguf(ctypes.byref(c), seed, None)
+    out = np.empty(n, dtype=np.uint8)
+    lib().vtqs_llama_gguf(ctypes.byref(c), seed, out.ctypes.data)
+    return out
+
+
+def tokens(seed: int, n: int, vocab: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint32)
+    lib().vtqs_tokens(seed, out.ctypes.data, n, vocab)
+    return out
+
+
+def e2e_inputs(cfg: dict = None, prompt_len: int = E2E_PROMPT):
+    """(gguf blob, prompt ids) of the end-to-end configuration."""
+    cfg = LLAMA_1B1 if cfg is None else cfg
+    blob = llama_gguf(cfg, SEED_BASE + E2E_INDEX)
+    prompt = tokens(SEED_BASE + E2E_INDEX + X_SEED_OFFSET, prompt_len, cfg["vocab"])
+    return blob, prompt
