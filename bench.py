@@ -55,6 +55,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-rotate", action="store_true", help="reuse one weight copy (MALL-warm figure)")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a replayed HIP graph")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run 20 device-to-device copies of this many MiB (HBM counter calibration)")
     return ap.parse_args()
@@ -198,19 +199,19 @@ def main():
     dw = [[torch.from_numpy(w).to(dev) for _ in range(copies)] for _, w in inputs]
     dy = [torch.empty(c.batch * c.out_feat, dtype=torch.float32, device=dev) for c in cfgs]
 
-    def launch(i, copy):
+    def launch(i, copy, sh):
         c = cfgs[i]
         ctx.linear_device(c.ggml_type, 0, dx[i].data_ptr(), dw[i][copy].data_ptr(), dw[i][copy].numel(),
                           dy[i].data_ptr(), c.batch, c.in_feat, c.out_feat, sh)
 
-    def step(k):
+    def step(k, sh):
         for i in range(len(cfgs)):
-            launch(i, k % copies)
+            launch(i, k % copies, sh)
 
     # parity of what is timed (outside the timed region)
     import oracle
 
-    step(0)
+    step(0, sh)
     torch.cuda.synchronize()
     bit_exact = True
     for i, c in enumerate(cfgs):
@@ -220,32 +221,39 @@ def main():
         bit_exact &= bool(np.array_equal(dy[i].cpu().numpy().view(np.uint32), want.view(np.uint32)))
 
     for k in range(args.warmup):
-        step(k)
+        step(k, sh)
     torch.cuda.synchronize()
 
-    # whole-step throughput: K steps bracketed by events
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for k in range(args.steps):
-        step(k)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_per_step = e0.elapsed_time(e1) / args.steps
+    def timed_us(body):
+        """Average GPU time of one body(k, stream) over args.steps calls, the
+        calls issued back to back.  Unless --eager, the calls are captured in
+        a HIP graph and replayed, so host launch overhead cannot leave the GPU
+        idle between kernels of a few microseconds."""
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        if args.eager:
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for k in range(args.steps):
+                body(k, sh)
+            e1.record(stream)
+        else:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                cs = torch.cuda.current_stream().cuda_stream
+                for k in range(args.steps):
+                    body(k, cs)
+            g.replay()
+            torch.cuda.synchronize()
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps * 1e3
 
-    # per-kernel average launch duration: K back-to-back launches of each
-    # config alone, bracketed by events on the launch stream (no per-launch
-    # event pairs, whose own overhead would inflate a ~10 us kernel)
-    launch_us = []
-    for i in range(len(cfgs)):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        a.record(stream)
-        for k in range(args.steps):
-            launch(i, k % copies)
-        b.record(stream)
-        torch.cuda.synchronize()
-        launch_us.append(a.elapsed_time(b) / args.steps * 1e3)
+    # whole-step throughput: K steps back to back
+    ms_per_step = timed_us(step) * 1e-3
+    # per-kernel average launch duration: K back-to-back launches of each config alone
+    launch_us = [timed_us(lambda k, s, i=i: launch(i, k % copies, s)) for i in range(len(cfgs))]
 
     step_bytes = sum(c.algorithmic_bytes() for c in cfgs)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9

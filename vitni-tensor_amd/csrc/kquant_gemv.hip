@@ -4,21 +4,34 @@
 // :1149-1196) and linear_q6_k_integer[_parallel] (:1060-1146) for any batch;
 // each batch row is one grid.y slice.
 //
-// Work unit = one 16-super-block window of one weight row.  Lane 4g+k of a
-// wave handles quarter k of super-block 16w+g, so one unit is 2304
-// contiguous bytes of Q4_K (3360 of Q6_K) read by the 64 lanes.  Each wave
-// owns a contiguous range of rows and streams its units through a ring of D
-// register buffers: the loads of D units are in flight before the activation
-// is even quantized, and every computed unit immediately refills its slot.
-//
-// Per unit: integer sums with v_dot4_i32_i8 against the int8 activation held
-// in LDS, reduced over the 4 lanes of a block with DPP (exact in any order);
-// the per-block float epilogue evaluated exactly as the reference writes it;
-// then the pinned fixed_tree over the window's 16 blocks and over the row's
-// windows.  fixed_tree(p[0..R)) equals fixed_tree over 16-aligned windows of
+// Lane mapping (both kernels): a window is 16 consecutive super-blocks of one
+// weight row; lane 4g+k of a wave handles quarter k of the window's block g,
+// so the 64 lanes together read the window's 2304 (Q4_K) or 3360 (Q6_K)
+// contiguous bytes.  Per window: integer sums with v_dot4_i32_i8, reduced over
+// the 4 lanes of a block with DPP (exact in any order); the per-block float
+// epilogue evaluated exactly as the reference writes it; then the pinned
+// fixed_tree over the window's 16 blocks and over the row's windows.
+// fixed_tree(p[0..R)) equals fixed_tree over 16-aligned windows of
 // fixed_tree(window), because the first four levels of the reference's tree
 // only pair blocks inside an aligned window; padded slots hold -0.0, the
 // exact identity of +.
+//
+// Every workgroup quantizes the whole activation row into LDS
+// (quantize_block_q8, src/ops/quant.rs:750-771) before it can use a weight.
+//
+// kquant_rows_kernel (rows of at most 3 windows for Q4_K, in_feat <= 12288,
+// and 2 for Q6_K, in_feat <= 8192; matrices under 2 GiB): each
+// lane copies its activation quarter of every window from LDS into registers
+// once, then streams whole rows (all windows of a row per step, static window
+// indices) through a ring of D register buffers.  Rows are dealt to waves
+// round-robin, so at any moment the chip reads one contiguous band of the
+// matrix.  Weight loads are raw buffer loads: a slot past the wave's last row
+// gets an offset beyond the buffer's size, which the hardware answers with
+// zeros and no memory traffic, so every load stays unconditional (vmcnt
+// waits stay exact) without re-reading any row.
+//
+// kquant_windows_kernel (any in_feat up to 32768): the unit is one window;
+// the activation quarter is re-read from LDS per unit.
 #include "vtq_device.h"
 #include "vtq_kernels.h"
 
@@ -36,7 +49,7 @@ struct ActLds {
     float* d;      // [R*64] d of block b at [64b + any lane]
     int* s16;      // [R*64] sum of run r at [64b + 4r]
     int* s32;      // [R*64] bsum of sub-block j at [64b + 8j]
-    float* ws;     // [NW*16] per-wave window sums
+    float* ws;     // [NW*8] per-wave window sums (windows kernel)
 };
 
 // Byte offsets of the activation arrays; every array starts 16-byte aligned.
@@ -72,6 +85,29 @@ __device__ __forceinline__ void quantize_block_to_lds(float4 v, int b, const Act
     a.d[b * 64 + lane] = d;
 }
 
+// The activation blocks of wave `wave`: b = wave + kNW*j.  The first
+// kXPerWave are loaded by load_act (issued before any weight load), the rest
+// are loaded where they are quantized.
+__device__ __forceinline__ void load_act(float4 (&xv)[kXPerWave], const float* __restrict__ xb, int R, int wave) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < kXPerWave; j++) {
+        const int b = wave + kNW * j;
+        if (b < R) xv[j] = reinterpret_cast<const float4*>(xb + (size_t)b * 256)[lane];
+    }
+}
+__device__ __forceinline__ void quantize_act(const float4 (&xv)[kXPerWave], const float* __restrict__ xb, int R,
+                                             int wave, const ActLds& act) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < kXPerWave; j++) {
+        const int b = wave + kNW * j;
+        if (b < R) quantize_block_to_lds(xv[j], b, act);
+    }
+    for (int b = wave + kNW * kXPerWave; b < R; b += kNW)
+        quantize_block_to_lds(reinterpret_cast<const float4*>(xb + (size_t)b * 256)[lane], b, act);
+}
+
 // fixed_tree over the per-window sums wv[0..nwin) (stride form, static indices).
 __device__ __forceinline__ float window_tree(float (&wv)[kMaxWindows], int nwin) {
 #pragma unroll
@@ -81,6 +117,14 @@ __device__ __forceinline__ float window_tree(float (&wv)[kMaxWindows], int nwin)
             if (i + s < nwin) wv[i] = wv[i] + wv[i + s];
         }
     }
+    return wv[0];
+}
+template <int N>
+__device__ __forceinline__ float windows_tree(float (&wv)[N]) {
+#pragma unroll
+    for (int s = 1; s < N; s <<= 1)
+#pragma unroll
+        for (int i = 0; i + s < N; i += 2 * s) wv[i] = wv[i] + wv[i + s];
     return wv[0];
 }
 
@@ -107,54 +151,98 @@ __device__ __forceinline__ float window16_tree(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// ------------------------------------------------------- raw buffer loads
+
+// Descriptor word 3 for raw (untyped, stride 0) buffers on gfx9-family parts.
+constexpr int kBufferWord3 = 0x00020000;
+// A load at this offset or beyond is out of range for every buffer the rows
+// kernel accepts (size < 2 GiB): it returns zeros without touching memory.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load2(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+}
+
 // ------------------------------------------------------------------ Q4_K
 
 struct Q4K {
     static constexpr int kBytes = 144;
-    static constexpr int kMaxD = 4;
+    static constexpr int kRowsMaxWindows = 3;  // rows kernel without register spills
     struct Regs {
         uint4 hdr, qa, qb;
     };
+    // the lane's activation quarter: sub-blocks 2k (xl) and 2k+1 (xh) of block g
+    struct X {
+        uint32_t xl[8], xh[8];
+        int bs_lo, bs_hi;
+        float dx;
+    };
+    // get_scale_min_k4 (src/ops/quant.rs:267-276) for j = 2k, 2k+1, two
+    // bytes at a time, without branching on the lane's k:
+    //   j < 4:  sc = s[j] & 63,                       m = s[j+4] & 63
+    //   j >= 4: sc = (s[j+4] & 15) | (s[j-4] >> 6) << 4, m = (s[j+4] >> 4) | (s[j] >> 6) << 4
+    struct Lane {
+        int sh;
+        bool hi;
+        uint32_t lowmask, topmask;
+    };
+    __device__ static Lane lane_consts(int k) {
+        Lane c;
+        c.sh = 16 * (k & 1);
+        c.hi = k >= 2;
+        c.lowmask = c.hi ? 0x0F0Fu : 0x3F3Fu;
+        c.topmask = c.hi ? 0x3030u : 0u;
+        return c;
+    }
     __device__ static void load(Regs& r, const uint8_t* __restrict__ blk, int k) {
         r.hdr = *reinterpret_cast<const uint4*>(blk);
         r.qa = *reinterpret_cast<const uint4*>(blk + 16 + 32 * k);
         r.qb = *reinterpret_cast<const uint4*>(blk + 32 + 32 * k);
     }
+    __device__ static void bload(Regs& r, __amdgpu_buffer_rsrc_t rs, uint32_t off, int k) {
+        r.hdr = buf_load16(rs, off);
+        r.qa = buf_load16(rs, off + 16 + 32 * k);
+        r.qb = buf_load16(rs, off + 32 + 32 * k);
+    }
+    __device__ static void load_x(X& x, const ActLds& act, int b, int k) {
+        const uint4* xw4 = reinterpret_cast<const uint4*>(act.qs + b * 64 + 16 * k);
+        const uint4 l0 = xw4[0], l1 = xw4[1], h0 = xw4[2], h1 = xw4[3];
+        x.xl[0] = l0.x; x.xl[1] = l0.y; x.xl[2] = l0.z; x.xl[3] = l0.w;
+        x.xl[4] = l1.x; x.xl[5] = l1.y; x.xl[6] = l1.z; x.xl[7] = l1.w;
+        x.xh[0] = h0.x; x.xh[1] = h0.y; x.xh[2] = h0.z; x.xh[3] = h0.w;
+        x.xh[4] = h1.x; x.xh[5] = h1.y; x.xh[6] = h1.z; x.xh[7] = h1.w;
+        x.bs_lo = act.s32[b * 64 + 16 * k];
+        x.bs_hi = act.s32[b * 64 + 16 * k + 8];
+        x.dx = act.d[b * 64];
+    }
     // dot_q4k_q8_block (src/ops/quant.rs:849-898) for quarter k = sub-blocks
     // 2k, 2k+1; returns this block's part (identical in the 4 lanes).
-    __device__ static float part(const Regs& r, const ActLds& act, int b, int k, bool valid) {
-        const uint4* xw4 = reinterpret_cast<const uint4*>(act.qs + b * 64 + 16 * k);
-        const uint4 xl0 = xw4[0], xl1 = xw4[1], xh0 = xw4[2], xh1 = xw4[3];
+    __device__ static float part(const Regs& r, const X& x, const Lane& c, bool valid) {
         const uint32_t qw[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
-        const uint32_t xl[8] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w};
-        const uint32_t xh[8] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w};
         int s_lo = 0, s_hi = 0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            s_lo = __builtin_amdgcn_sdot4((int)(qw[i] & 0x0F0F0F0Fu), (int)xl[i], s_lo, false);
-            s_hi = __builtin_amdgcn_sdot4((int)((qw[i] >> 4) & 0x0F0F0F0Fu), (int)xh[i], s_hi, false);
+            s_lo = __builtin_amdgcn_sdot4((int)(qw[i] & 0x0F0F0F0Fu), (int)x.xl[i], s_lo, false);
+            s_hi = __builtin_amdgcn_sdot4((int)((qw[i] >> 4) & 0x0F0F0F0Fu), (int)x.xh[i], s_hi, false);
         }
-        // get_scale_min_k4 (src/ops/quant.rs:267-276) for j = 2k, 2k+1, two
-        // bytes at a time, without branching on the lane's k:
-        //   j < 4:  sc = s[j] & 63,                       m = s[j+4] & 63
-        //   j >= 4: sc = (s[j+4] & 15) | (s[j-4] >> 6) << 4, m = (s[j+4] >> 4) | (s[j] >> 6) << 4
-        const int sh = 16 * (k & 1);
-        const bool hi = k >= 2;
-        const uint32_t A = r.hdr.w >> sh, B = r.hdr.y >> sh, C = r.hdr.z >> sh;
-        const uint32_t lowmask = hi ? 0x0F0Fu : 0x3F3Fu, topmask = hi ? 0x3030u : 0u;
-        const uint32_t scp = ((hi ? A : B) & lowmask) | ((B >> 2) & topmask);
-        const uint32_t mp = ((hi ? (A >> 4) : C) & lowmask) | ((C >> 2) & topmask);
-        const int bs_lo = act.s32[b * 64 + 16 * k], bs_hi = act.s32[b * 64 + 16 * k + 8];
+        const uint32_t A = r.hdr.w >> c.sh, B = r.hdr.y >> c.sh, C = r.hdr.z >> c.sh;
+        const uint32_t scp = ((c.hi ? A : B) & c.lowmask) | ((B >> 2) & c.topmask);
+        const uint32_t mp = ((c.hi ? (A >> 4) : C) & c.lowmask) | ((C >> 2) & c.topmask);
         // every factor fits 24 bits (sc, m <= 63; |s| <= 60960; |bsum| <= 4064): full-rate v_mad_i32_i24
         int acc = __mul24((int)(scp & 0xFFu), s_lo) + __mul24((int)(scp >> 8), s_hi);
-        int accm = __mul24((int)(mp & 0xFFu), bs_lo) + __mul24((int)(mp >> 8), bs_hi);
+        int accm = __mul24((int)(mp & 0xFFu), x.bs_lo) + __mul24((int)(mp >> 8), x.bs_hi);
         acc = quad_sum_i(acc);
         accm = quad_sum_i(accm);
-        const float dx = act.d[b * 64];
         const float d = f16_hw(r.hdr.x & 0xFFFFu);
         const float dmin = f16_hw(r.hdr.x >> 16);
-        const float t1 = (d * dx) * (float)acc;
-        const float t2 = (dmin * dx) * (float)accm;
+        const float t1 = (d * x.dx) * (float)acc;
+        const float t2 = (dmin * x.dx) * (float)accm;
         return valid ? t1 - t2 : -0.0f;
     }
 };
@@ -164,28 +252,46 @@ struct Q4K {
 // 16 bytes from a 2-byte-aligned address p, as five aligned dwords from
 // p & ~3 funnel-shifted by (p & 3) bytes.  Reads [p - (p&3), p - (p&3) + 20),
 // which for the runs used below stays inside the 210-byte block.
+__device__ __forceinline__ uint4 funnel16(u32x4_a4 v, uint32_t e, uint32_t off) {
+    return make_uint4(__builtin_amdgcn_alignbyte(v.y, v.x, off), __builtin_amdgcn_alignbyte(v.z, v.y, off),
+                      __builtin_amdgcn_alignbyte(v.w, v.z, off), __builtin_amdgcn_alignbyte(e, v.w, off));
+}
 __device__ __forceinline__ uint4 load16_a2(const uint8_t* p) {
     // pointer arithmetic (not an integer round trip) keeps the global address
     // space visible to the compiler: global_load, not flat_load
     const uint32_t off = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
     const uint32_t* p4 = reinterpret_cast<const uint32_t*>(p - off);
-    const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(p4);
-    const uint32_t e = p4[4];
-    return make_uint4(__builtin_amdgcn_alignbyte(v.y, v.x, off), __builtin_amdgcn_alignbyte(v.z, v.y, off),
-                      __builtin_amdgcn_alignbyte(v.w, v.z, off), __builtin_amdgcn_alignbyte(e, v.w, off));
+    return funnel16(*reinterpret_cast<const u32x4_a4*>(p4), p4[4], off);
+}
+// The same from a buffer whose base is 16-byte aligned.
+__device__ __forceinline__ uint4 buf_load16_a2(__amdgpu_buffer_rsrc_t rs, uint32_t p) {
+    const uint32_t off = p & 3u, a = p - off;
+    const u32x4_a4 v = __builtin_bit_cast(u32x4_a4, __builtin_amdgcn_raw_buffer_load_b128(rs, a, 0, 0));
+    return funnel16(v, buf_load4(rs, a + 16), off);
 }
 
 __device__ __forceinline__ int sext8(uint32_t v, int byte) { return (int)(int8_t)((v >> (8 * byte)) & 0xFFu); }
 
 struct Q6K {
     static constexpr int kBytes = 210;
-    static constexpr int kMaxD = 2;
+    static constexpr int kRowsMaxWindows = 2;
     struct Regs {
         uint4 b0, b1, hh;
         uint4 sc;      // scale bytes 192..207 (funnel-shifted)
         uint32_t d;    // f16 bits of d
     };
+    // the lane's activation: runs 8hf+t+2q (q = 0..3) of block g, with
+    // m_q = 32 * (sum of run q) to fold the code offset -32 in exactly
+    struct X {
+        uint4 x1, x2, x3, x4;
+        int m1, m2, m3, m4;
+        float dx;
+    };
     // Lane k: hf = k>>1 (128-element half), t = k&1 (positions l in [16t, 16t+16)).
+    struct Lane {
+        int hf, t;
+    };
+    __device__ static Lane lane_consts(int k) { return Lane{k >> 1, k & 1}; }
     // Reads stay inside the block: ql/qh runs end by byte 196, the scale
     // dwords start at 192 - (blk&3) and two ushorts read bytes 206..209.
     __device__ static void load(Regs& r, const uint8_t* __restrict__ blk, int k) {
@@ -196,26 +302,44 @@ struct Q6K {
         const uint32_t off = (uint32_t)(reinterpret_cast<uintptr_t>(blk + 192) & 3u);
         const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(blk + 192 - off);
         const uint32_t tail = *reinterpret_cast<const uint16_t*>(blk + 206);  // bytes 206, 207
-        r.sc = make_uint4(__builtin_amdgcn_alignbyte(v.y, v.x, off), __builtin_amdgcn_alignbyte(v.z, v.y, off),
-                          __builtin_amdgcn_alignbyte(v.w, v.z, off), __builtin_amdgcn_alignbyte(tail, v.w, off));
+        r.sc = funnel16(v, tail, off);
         r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
+    }
+    __device__ static void bload(Regs& r, __amdgpu_buffer_rsrc_t rs, uint32_t blk, int k) {
+        const int hf = k >> 1, t = k & 1;
+        r.b0 = buf_load16_a2(rs, blk + 64 * hf + 16 * t);
+        r.b1 = buf_load16_a2(rs, blk + 64 * hf + 32 + 16 * t);
+        r.hh = buf_load16_a2(rs, blk + 128 + 32 * hf + 16 * t);
+        const uint32_t off = (blk + 192) & 3u;
+        const u32x4_a4 v = __builtin_bit_cast(u32x4_a4, __builtin_amdgcn_raw_buffer_load_b128(rs, blk + 192 - off, 0, 0));
+        r.sc = funnel16(v, buf_load2(rs, blk + 206), off);
+        r.d = buf_load2(rs, blk + 208);
+    }
+    // activation words: element 128hf + 16t + 32q + 4i -> word 32hf + 4t + 8q + i;
+    // run (bucket) of q is 8hf + t + 2q, its sum sits at lane 4 * run
+    __device__ static void load_x(X& x, const ActLds& act, int b, int k) {
+        const int hf = k >> 1, t = k & 1;
+        const uint32_t* xw = act.qs + b * 64 + 32 * hf + 4 * t;
+        x.x1 = *reinterpret_cast<const uint4*>(xw);
+        x.x2 = *reinterpret_cast<const uint4*>(xw + 8);
+        x.x3 = *reinterpret_cast<const uint4*>(xw + 16);
+        x.x4 = *reinterpret_cast<const uint4*>(xw + 24);
+        const int* s16 = act.s16 + b * 64 + 4 * (8 * hf + t);
+        x.m1 = 32 * s16[0];
+        x.m2 = 32 * s16[8];
+        x.m3 = 32 * s16[16];
+        x.m4 = 32 * s16[24];
+        x.dx = act.d[b * 64];
     }
     // dot_q6k_q8_block (src/ops/quant.rs:995-1057): buckets 8hf+t+2q (q = 0..3)
     // are exactly one 16-element run each; (code - 32) is folded in as
     // sum(code*x) - 32*sum(x) with the run sums from the activation pass.
-    __device__ static float part(const Regs& r, const ActLds& act, int b, int k, bool valid) {
-        const int hf = k >> 1, t = k & 1;
-        // activation words: element 128hf + 16t + 32q + 4i -> word 32hf + 4t + 8q + i
-        const uint32_t* xw = act.qs + b * 64 + 32 * hf + 4 * t;
-        const uint4 x1 = *reinterpret_cast<const uint4*>(xw);
-        const uint4 x2 = *reinterpret_cast<const uint4*>(xw + 8);
-        const uint4 x3 = *reinterpret_cast<const uint4*>(xw + 16);
-        const uint4 x4 = *reinterpret_cast<const uint4*>(xw + 24);
+    __device__ static float part(const Regs& r, const X& x, const Lane& c, bool valid) {
         const uint32_t B0[4] = {r.b0.x, r.b0.y, r.b0.z, r.b0.w};
         const uint32_t B1[4] = {r.b1.x, r.b1.y, r.b1.z, r.b1.w};
         const uint32_t H[4] = {r.hh.x, r.hh.y, r.hh.z, r.hh.w};
-        const uint32_t X1[4] = {x1.x, x1.y, x1.z, x1.w}, X2[4] = {x2.x, x2.y, x2.z, x2.w};
-        const uint32_t X3[4] = {x3.x, x3.y, x3.z, x3.w}, X4[4] = {x4.x, x4.y, x4.z, x4.w};
+        const uint32_t X1[4] = {x.x1.x, x.x1.y, x.x1.z, x.x1.w}, X2[4] = {x.x2.x, x.x2.y, x.x2.z, x.x2.w};
+        const uint32_t X3[4] = {x.x3.x, x.x3.y, x.x3.z, x.x3.w}, X4[4] = {x.x4.x, x.x4.y, x.x4.z, x.x4.w};
         int S1 = 0, S2 = 0, S3 = 0, S4 = 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -228,24 +352,91 @@ struct Q6K {
             S3 = __builtin_amdgcn_sdot4((int)q3, (int)X3[i], S3, false);
             S4 = __builtin_amdgcn_sdot4((int)q4, (int)X4[i], S4, false);
         }
-        // run (bucket) of q1 is 8hf + t, q2..q4 at +2, +4, +6; run r sits at lane 4r
-        const int* s16 = act.s16 + b * 64 + 4 * (8 * hf + t);
-        const int sum1 = S1 - 32 * s16[0];
-        const int sum2 = S2 - 32 * s16[8];
-        const int sum3 = S3 - 32 * s16[16];
-        const int sum4 = S4 - 32 * s16[24];
+        const int sum1 = S1 - x.m1, sum2 = S2 - x.m2, sum3 = S3 - x.m3, sum4 = S4 - x.m4;
         // scales: i8 at 192 + 8hf + t + 2q -> bytes t, t+2 of dwords 2hf and 2hf+1
-        const uint32_t sa = hf ? r.sc.z : r.sc.x, sb = hf ? r.sc.w : r.sc.y;
+        const uint32_t sa = c.hf ? r.sc.z : r.sc.x, sb = c.hf ? r.sc.w : r.sc.y;
         // |sc| <= 64 and |sum| <= 16*31*127: every product fits v_mad_i32_i24
-        int acc = __mul24(sext8(sa, t), sum1) + __mul24(sext8(sa, t + 2), sum2) +
-                  __mul24(sext8(sb, t), sum3) + __mul24(sext8(sb, t + 2), sum4);
+        int acc = __mul24(sext8(sa, c.t), sum1) + __mul24(sext8(sa, c.t + 2), sum2) +
+                  __mul24(sext8(sb, c.t), sum3) + __mul24(sext8(sb, c.t + 2), sum4);
         acc = quad_sum_i(acc);
         const float d = f16_hw(r.d);
-        return valid ? (d * act.d[b * 64]) * (float)acc : -0.0f;
+        return valid ? (d * x.dx) * (float)acc : -0.0f;
     }
 };
 
-// --------------------------------------------------------------- kernel
+// ------------------------------------------------------------ rows kernel
+
+// Row j of wave gw is gw + j*tw (tw = waves in the grid); lane j keeps that
+// row's result and the wave stores its rows once at the end.  PRE of the D
+// ring slots are loaded before the activation is quantized (their data then
+// shares the memory system with the activation reads), the rest after.
+template <class Fmt, int NWIN, int D, int PRE>
+__global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __restrict__ x,
+                                                               const uint8_t* __restrict__ W,
+                                                               float* __restrict__ y, int R, int out_feat) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const ActLds act = act_lds_layout(lds, R);
+    const int lane = threadIdx.x & 63;
+    const int wave = wave_id();
+    const int g = lane >> 2, k = lane & 3;
+    const float* xb = x + (size_t)blockIdx.y * R * 256;
+    float* yb = y + (size_t)blockIdx.y * out_feat;
+    const uint32_t row_bytes = (uint32_t)R * Fmt::kBytes;
+    const int tw = gridDim.x * kNW, gw = blockIdx.x * kNW + wave;
+    const int nrows = gw < out_feat ? (out_feat - 1 - gw) / tw + 1 : 0;  // <= 64 (launcher)
+
+    float4 xv[kXPerWave];
+    load_act(xv, xb, R, wave);
+
+    uint32_t boff[NWIN];
+    bool valid[NWIN];
+#pragma unroll
+    for (int w = 0; w < NWIN; w++) {
+        const int b = 16 * w + g;
+        valid[w] = b < R;
+        boff[w] = (uint32_t)(b < R ? b : R - 1) * Fmt::kBytes;
+    }
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, (int)(row_bytes * (uint32_t)out_feat),
+                                          kBufferWord3);
+    typename Fmt::Regs buf[D][NWIN];
+    auto load_row = [&](typename Fmt::Regs (&rb)[NWIN], int j) {
+        const uint32_t ro = j < nrows ? (uint32_t)(gw + j * tw) * row_bytes : kOutOfRange;
+#pragma unroll
+        for (int w = 0; w < NWIN; w++) Fmt::bload(rb[w], rs, ro + boff[w], k);
+    };
+#pragma unroll
+    for (int i = 0; i < PRE; i++) load_row(buf[i], i);
+    // keep the x-dependent math (and its wait on the x loads) below the weight loads just issued
+    __builtin_amdgcn_sched_barrier(0);
+    quantize_act(xv, xb, R, wave, act);
+    __syncthreads();
+
+    typename Fmt::X xr[NWIN];
+#pragma unroll
+    for (int w = 0; w < NWIN; w++) Fmt::load_x(xr[w], act, 16 * w + g < R ? 16 * w + g : R - 1, k);
+    const typename Fmt::Lane lc = Fmt::lane_consts(k);
+#pragma unroll
+    for (int i = PRE; i < D; i++) load_row(buf[i], i);
+
+    float yacc = 0.0f;
+    for (int j0 = 0; j0 < nrows; j0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; i++) {
+            if (j0 + i < nrows) {
+                float wv[NWIN];
+#pragma unroll
+                for (int w = 0; w < NWIN; w++) wv[w] = window16_tree(Fmt::part(buf[i][w], xr[w], lc, valid[w]));
+                const float rv = windows_tree<NWIN>(wv);
+                yacc = (lane == j0 + i) ? rv : yacc;
+            }
+            load_row(buf[i], j0 + i + D);
+        }
+    }
+    if (lane < nrows) yb[gw + lane * tw] = yacc;
+}
+
+// ---------------------------------------------------------- windows kernel
 
 // Every global load below is issued unconditionally (lanes of padded
 // blocks and slots past a wave's last unit read a clamped, valid address and
@@ -254,9 +445,9 @@ struct Q6K {
 // straight-line loads each wait covers exactly the data it needs.  Results
 // are kept in registers and stored once at the end for the same reason.
 template <class Fmt, int D>
-__global__ __launch_bounds__(kNW * 64) void kquant_gemv_kernel(const float* __restrict__ x,
-                                                               const uint8_t* __restrict__ W,
-                                                               float* __restrict__ y, int R, int out_feat) {
+__global__ __launch_bounds__(kNW * 64) void kquant_windows_kernel(const float* __restrict__ x,
+                                                                  const uint8_t* __restrict__ W,
+                                                                  float* __restrict__ y, int R, int out_feat) {
     extern __shared__ __align__(16) unsigned char lds[];
     const ActLds act = act_lds_layout(lds, R);
     const int lane = threadIdx.x & 63;
@@ -277,11 +468,7 @@ __global__ __launch_bounds__(kNW * 64) void kquant_gemv_kernel(const float* __re
 
     // 1. activation loads first (older than every weight load)
     float4 xv[kXPerWave];
-#pragma unroll
-    for (int j = 0; j < kXPerWave; j++) {
-        const int b = wave + kNW * j;
-        if (b < R) xv[j] = reinterpret_cast<const float4*>(xb + (size_t)b * 256)[lane];
-    }
+    load_act(xv, xb, R, wave);
 
     float yacc = 0.0f;  // lane i keeps the result of row r0 + i
     int crow = 0, cw = 0;
@@ -308,14 +495,9 @@ __global__ __launch_bounds__(kNW * 64) void kquant_gemv_kernel(const float* __re
     // scheduling barrier keeps the x-dependent math (and its wait on the x
     // loads) below the weight loads just issued.
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < kXPerWave; j++) {
-        const int b = wave + kNW * j;
-        if (b < R) quantize_block_to_lds(xv[j], b, act);
-    }
-    for (int b = wave + kNW * kXPerWave; b < R; b += kNW)
-        quantize_block_to_lds(reinterpret_cast<const float4*>(xb + (size_t)b * 256)[lane], b, act);
+    quantize_act(xv, xb, R, wave, act);
     __syncthreads();
+    const typename Fmt::Lane lc = Fmt::lane_consts(k);
 
     // 4. compute each chunk of D units, then load the next one
     for (int u0 = 0;; u0 += D) {
@@ -323,8 +505,9 @@ __global__ __launch_bounds__(kNW * 64) void kquant_gemv_kernel(const float* __re
         for (int i = 0; i < D; i++) {
             if (u0 + i < nunits) {
                 const int b = 16 * cw + g;
-                const float part = Fmt::part(buf[i], act, b < R ? b : R - 1, k, b < R);
-                const float s = window16_tree(part);
+                typename Fmt::X xr;
+                Fmt::load_x(xr, act, b < R ? b : R - 1, k);
+                const float s = window16_tree(Fmt::part(buf[i], xr, lc, b < R));
                 float rv = s;
                 if (nwin > 1) {
                     float* ws = act.ws + wave * kMaxWindows;
@@ -360,14 +543,29 @@ static hipError_t allow_lds(K kernel, size_t bytes) {
                                (int)bytes);
 }
 
-template <class Fmt, int D>
-static hipError_t launch_kq_d(const float* x, const uint8_t* w, float* y, int batch, int R, int out_feat, int wgs,
-                              hipStream_t stream) {
-    auto kern = kquant_gemv_kernel<Fmt, D>;
+template <class K>
+static hipError_t launch(K kern, int wgs, int batch, int R, const float* x, const uint8_t* w, float* y, int out_feat,
+                         hipStream_t stream) {
     if (hipError_t e = allow_lds(kern, act_lds_bytes(R))) return e;
     hipLaunchKernelGGL(kern, dim3((unsigned)wgs, (unsigned)batch, 1), dim3(kNW * 64), act_lds_bytes(R), stream, x,
                        w, y, R, out_feat);
     return hipGetLastError();
+}
+
+// Ring depth D and pre-quantization loads PRE of the rows kernel: one-window
+// rows keep two rows in flight, one of them issued before the activation
+// pass; longer rows keep a single row in flight, issued after it (Q4_K
+// two-window rows still fit two).  Deeper rings spill registers.
+template <class Fmt>
+static hipError_t launch_rows(int nwin, int wgs, int batch, int R, const float* x, const uint8_t* w, float* y,
+                              int out_feat, hipStream_t stream) {
+    if (nwin == 1) return launch(kquant_rows_kernel<Fmt, 1, 2, 1>, wgs, batch, R, x, w, y, out_feat, stream);
+    if constexpr (Fmt::kRowsMaxWindows == 2) {
+        return launch(kquant_rows_kernel<Fmt, 2, 1, 0>, wgs, batch, R, x, w, y, out_feat, stream);
+    } else {
+        if (nwin == 2) return launch(kquant_rows_kernel<Fmt, 2, 2, 1>, wgs, batch, R, x, w, y, out_feat, stream);
+        return launch(kquant_rows_kernel<Fmt, 3, 1, 0>, wgs, batch, R, x, w, y, out_feat, stream);
+    }
 }
 
 template <class Fmt>
@@ -379,12 +577,20 @@ static hipError_t launch_kq(const float* x, const uint8_t* w, float* y, int batc
     int wgs = num_cus;
     const int need = (out_feat + kNW * 64 - 1) / (kNW * 64);
     if (wgs < need) wgs = need;
+    const size_t bytes = (size_t)out_feat * R * Fmt::kBytes;
+    if (nwin <= Fmt::kRowsMaxWindows && bytes < (size_t)kOutOfRange)
+        return launch_rows<Fmt>(nwin, wgs, batch, R, x, w, y, out_feat, stream);
     const long waves = (long)wgs * kNW;
     const long units = ((long)out_feat + waves - 1) / waves * nwin;  // per wave, upper bound
-    // 16 waves per CU leave 128 VGPRs per wave: at most kMaxD units in flight
-    if (units <= 1 || Fmt::kMaxD == 1) return launch_kq_d<Fmt, 1>(x, w, y, batch, R, out_feat, wgs, stream);
-    if (units <= 2 || Fmt::kMaxD == 2) return launch_kq_d<Fmt, 2>(x, w, y, batch, R, out_feat, wgs, stream);
-    return launch_kq_d<Fmt, 4>(x, w, y, batch, R, out_feat, wgs, stream);
+    // 16 waves per CU leave 128 VGPRs per wave: at most 4 (Q4_K) / 2 (Q6_K) units in flight
+    constexpr int kMaxD = sizeof(typename Fmt::Regs) > 48 ? 2 : 4;
+    if (units <= 1) return launch(kquant_windows_kernel<Fmt, 1>, wgs, batch, R, x, w, y, out_feat, stream);
+    if constexpr (kMaxD == 2) {
+        return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, x, w, y, out_feat, stream);
+    } else {
+        if (units <= 2) return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, x, w, y, out_feat, stream);
+        return launch(kquant_windows_kernel<Fmt, 4>, wgs, batch, R, x, w, y, out_feat, stream);
+    }
 }
 
 hipError_t launch_q4k_gemv(const float* x, const uint8_t* w, float* y, int batch, int in_feat, int out_feat,
