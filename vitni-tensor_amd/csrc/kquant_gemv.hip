@@ -34,6 +34,9 @@
 // the activation quarter is re-read from LDS per unit.
 #include "vtq_device.h"
 #include "vtq_kernels.h"
+#include "vtq_libm.h"
+
+#include <type_traits>
 
 namespace vtq {
 
@@ -70,7 +73,8 @@ __device__ __forceinline__ ActLds act_lds_layout(unsigned char* base, int R) {
 
 constexpr int kNW = 16;        // waves per workgroup; one workgroup per CU
 constexpr int kXPerWave = 4;   // activation blocks each wave loads up front (R <= 64 fully overlapped)
-size_t act_lds_bytes(int R) { return act_off_ws(R) + kNW * kMaxWindows * 4; }
+__host__ __device__ constexpr size_t act_lds_end(int R) { return act_off_ws(R) + kNW * kMaxWindows * 4; }
+size_t act_lds_bytes(int R) { return act_lds_end(R); }
 
 // quantize_block_q8 (src/ops/quant.rs:750-771) of 256-block b, held as one
 // float4 per lane (elements 4L..4L+3), into the LDS activation arrays.
@@ -88,23 +92,25 @@ __device__ __forceinline__ void quantize_block_to_lds(float4 v, int b, const Act
 // The activation blocks of wave `wave`: b = wave + kNW*j.  The first
 // kXPerWave are loaded by load_act (issued before any weight load), the rest
 // are loaded where they are quantized.
-__device__ __forceinline__ void load_act(float4 (&xv)[kXPerWave], const float* __restrict__ xb, int R, int wave) {
+template <int XPW>
+__device__ __forceinline__ void load_act(float4 (&xv)[XPW], const float* __restrict__ xb, int R, int wave) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int j = 0; j < kXPerWave; j++) {
+    for (int j = 0; j < XPW; j++) {
         const int b = wave + kNW * j;
         if (b < R) xv[j] = reinterpret_cast<const float4*>(xb + (size_t)b * 256)[lane];
     }
 }
-__device__ __forceinline__ void quantize_act(const float4 (&xv)[kXPerWave], const float* __restrict__ xb, int R,
-                                             int wave, const ActLds& act) {
+template <int XPW>
+__device__ __forceinline__ void quantize_act(const float4 (&xv)[XPW], const float* __restrict__ xb, int R, int wave,
+                                             const ActLds& act) {
     const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int j = 0; j < kXPerWave; j++) {
+    for (int j = 0; j < XPW; j++) {
         const int b = wave + kNW * j;
         if (b < R) quantize_block_to_lds(xv[j], b, act);
     }
-    for (int b = wave + kNW * kXPerWave; b < R; b += kNW)
+    for (int b = wave + kNW * XPW; b < R; b += kNW)
         quantize_block_to_lds(reinterpret_cast<const float4*>(xb + (size_t)b * 256)[lane], b, act);
 }
 
@@ -370,23 +376,34 @@ struct Q6K {
 // row's result and the wave stores its rows once at the end.  PRE of the D
 // ring slots are loaded before the activation is quantized (their data then
 // shares the memory system with the activation reads), the rest after.
-template <class Fmt, int NWIN, int D, int PRE>
-__global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __restrict__ x,
-                                                               const uint8_t* __restrict__ W,
-                                                               float* __restrict__ y, int R, int out_feat) {
+//
+// The output rows are the concatenation of up to three weight matrices that
+// share the activation (RowsArgs); EPI selects what is stored:
+//   kEpiStore       y[r] = row r . x
+//   kEpiAccumulate  y[r] = y[r] + row r . x   (the reference's residual add)
+//   kEpiSwiGLU      two matrices of equal rows; y[i] = silu(g) * u with
+//                   g = W0 row i . x, u = W1 row i . x and silu(g) =
+//                   g / (1 + expf(-g))  (forward_quantized.rs SwiGLU)
+template <class Fmt, int NWIN, int D, int PRE, int EPI, bool MULTI, bool NORM>
+__global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __restrict__ x, RowsArgs args,
+                                                               float* __restrict__ y, int R) {
+    constexpr int NM = EPI == kEpiSwiGLU ? 2 : 1;  // matrices read per output row
     extern __shared__ __align__(16) unsigned char lds[];
     const ActLds act = act_lds_layout(lds, R);
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
     const int g = lane >> 2, k = lane & 3;
+    const int out_feat = EPI == kEpiSwiGLU ? args.rows[0] : args.rows[0] + args.rows[1] + args.rows[2];
     const float* xb = x + (size_t)blockIdx.y * R * 256;
     float* yb = y + (size_t)blockIdx.y * out_feat;
     const uint32_t row_bytes = (uint32_t)R * Fmt::kBytes;
     const int tw = gridDim.x * kNW, gw = blockIdx.x * kNW + wave;
     const int nrows = gw < out_feat ? (out_feat - 1 - gw) / tw + 1 : 0;  // <= 64 (launcher)
 
-    float4 xv[kXPerWave];
+    // R <= 16 * NWIN: each wave holds at most NWIN activation blocks
+    float4 xv[NWIN], nw[NWIN];
     load_act(xv, xb, R, wave);
+    if constexpr (NORM) load_act(nw, args.norm_w, R, wave);
 
     uint32_t boff[NWIN];
     bool valid[NWIN];
@@ -396,19 +413,74 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
         valid[w] = b < R;
         boff[w] = (uint32_t)(b < R ? b : R - 1) * Fmt::kBytes;
     }
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, (int)(row_bytes * (uint32_t)out_feat),
-                                          kBufferWord3);
-    typename Fmt::Regs buf[D][NWIN];
-    auto load_row = [&](typename Fmt::Regs (&rb)[NWIN], int j) {
-        const uint32_t ro = j < nrows ? (uint32_t)(gw + j * tw) * row_bytes : kOutOfRange;
+    auto rsrc = [&](const uint8_t* w, int rows) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(w), (short)0, (int)(row_bytes * (uint32_t)rows),
+                                                 kBufferWord3);
+    };
+    const int c1 = args.rows[0], c2 = args.rows[0] + args.rows[1];
+    typename Fmt::Regs buf[D][NM][NWIN];
+    auto load_row = [&](typename Fmt::Regs (&rb)[NM][NWIN], int j) {
+        const int r = gw + j * tw;
+        if constexpr (EPI == kEpiSwiGLU) {
+            const uint32_t ro = j < nrows ? (uint32_t)r * row_bytes : kOutOfRange;
 #pragma unroll
-        for (int w = 0; w < NWIN; w++) Fmt::bload(rb[w], rs, ro + boff[w], k);
+            for (int m = 0; m < 2; m++) {
+                const __amdgpu_buffer_rsrc_t rs = rsrc(args.w[m], args.rows[m]);
+#pragma unroll
+                for (int w = 0; w < NWIN; w++) Fmt::bload(rb[m][w], rs, ro + boff[w], k);
+            }
+        } else if constexpr (!MULTI) {
+            const uint32_t ro = j < nrows ? (uint32_t)r * row_bytes : kOutOfRange;
+            const __amdgpu_buffer_rsrc_t rs = rsrc(args.w[0], args.rows[0]);
+#pragma unroll
+            for (int w = 0; w < NWIN; w++) Fmt::bload(rb[0][w], rs, ro + boff[w], k);
+        } else {
+            // segment of row r (wave-uniform): the matrix and the row inside it
+            const int sg = (r >= c1) + (r >= c2);
+            const int lr = r - (sg == 0 ? 0 : sg == 1 ? c1 : c2);
+            const uint32_t ro = j < nrows ? (uint32_t)lr * row_bytes : kOutOfRange;
+            const __amdgpu_buffer_rsrc_t rsel = rsrc(sg == 0 ? args.w[0] : sg == 1 ? args.w[1] : args.w[2],
+                                                     sg == 0 ? args.rows[0] : sg == 1 ? args.rows[1] : args.rows[2]);
+#pragma unroll
+            for (int w = 0; w < NWIN; w++) Fmt::bload(rb[0][w], rsel, ro + boff[w], k);
+        }
     };
 #pragma unroll
     for (int i = 0; i < PRE; i++) load_row(buf[i], i);
     // keep the x-dependent math (and its wait on the x loads) below the weight loads just issued
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (NORM) {
+        // rms_norm_slice: x*x per element into LDS past the activation arrays
+        // (in the layout serial_sum_bcast reads), the sum of squares serially
+        // by wave 0, then x * scale * w
+        float* prod = reinterpret_cast<float*>(lds + act_lds_end(R));
+#pragma unroll
+        for (int j = 0; j < NWIN; j++) {
+            const int b = wave + kNW * j;
+            const float4 v = xv[j];
+            if (b < R) {
+                const float sq[4] = {v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int i = 4 * lane + e;  // element 256b + i
+                    prod[256 * b + 16 * (i & 15) + (i >> 4)] = sq[e];
+                }
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const float sumsq = serial_sum_bcast(prod, R);
+            const float mean = sumsq / (float)(R * 256);
+            if (lane == 0) prod[R * 256] = 1.0f / libm::sqrtf(mean + args.eps);
+        }
+        __syncthreads();
+        const float scale = prod[R * 256];
+#pragma unroll
+        for (int j = 0; j < NWIN; j++) {
+            const float4 v = xv[j], w = nw[j];
+            xv[j] = make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z, v.w * scale * w.w);
+        }
+    }
     quantize_act(xv, xb, R, wave, act);
     __syncthreads();
 
@@ -424,16 +496,29 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
 #pragma unroll
         for (int i = 0; i < D; i++) {
             if (j0 + i < nrows) {
-                float wv[NWIN];
+                float rv[NM];
 #pragma unroll
-                for (int w = 0; w < NWIN; w++) wv[w] = window16_tree(Fmt::part(buf[i][w], xr[w], lc, valid[w]));
-                const float rv = windows_tree<NWIN>(wv);
-                yacc = (lane == j0 + i) ? rv : yacc;
+                for (int m = 0; m < NM; m++) {
+                    float wv[NWIN];
+#pragma unroll
+                    for (int w = 0; w < NWIN; w++)
+                        wv[w] = window16_tree(Fmt::part(buf[i][m][w], xr[w], lc, valid[w]));
+                    rv[m] = windows_tree<NWIN>(wv);
+                }
+                float v = rv[0];
+                if constexpr (EPI == kEpiSwiGLU) v = (rv[0] / (1.0f + libm::expf(-rv[0]))) * rv[1];
+                yacc = (lane == j0 + i) ? v : yacc;
             }
             load_row(buf[i], j0 + i + D);
         }
     }
-    if (lane < nrows) yb[gw + lane * tw] = yacc;
+    if (lane < nrows) {
+        float* yp = yb + gw + lane * tw;
+        if constexpr (EPI == kEpiAccumulate)
+            *yp = *yp + yacc;
+        else
+            *yp = yacc;
+    }
 }
 
 // ---------------------------------------------------------- windows kernel
@@ -543,28 +628,44 @@ static hipError_t allow_lds(K kernel, size_t bytes) {
                                (int)bytes);
 }
 
-template <class K>
-static hipError_t launch(K kern, int wgs, int batch, int R, const float* x, const uint8_t* w, float* y, int out_feat,
-                         hipStream_t stream) {
-    if (hipError_t e = allow_lds(kern, act_lds_bytes(R))) return e;
-    hipLaunchKernelGGL(kern, dim3((unsigned)wgs, (unsigned)batch, 1), dim3(kNW * 64), act_lds_bytes(R), stream, x,
-                       w, y, R, out_feat);
+template <class K, class... A>
+static hipError_t launch_lds(K kern, int wgs, int batch, size_t lds, hipStream_t stream, A... a) {
+    if (hipError_t e = allow_lds(kern, lds)) return e;
+    hipLaunchKernelGGL(kern, dim3((unsigned)wgs, (unsigned)batch, 1), dim3(kNW * 64), lds, stream, a...);
     return hipGetLastError();
+}
+template <class K, class... A>
+static hipError_t launch(K kern, int wgs, int batch, int R, hipStream_t stream, A... a) {
+    return launch_lds(kern, wgs, batch, act_lds_bytes(R), stream, a...);
+}
+// the normalising prologue keeps R*256 products and the scale past the activation arrays
+static size_t norm_lds_bytes(int R) { return act_lds_bytes(R) + (size_t)R * 1024 + 16; }
+
+// one 16-wave workgroup per CU; more if a wave would own over 64 rows
+static int rows_grid(int out_feat, int num_cus) {
+    const int need = (out_feat + kNW * 64 - 1) / (kNW * 64);
+    return num_cus < need ? need : num_cus;
 }
 
 // Ring depth D and pre-quantization loads PRE of the rows kernel: one-window
 // rows keep two rows in flight, one of them issued before the activation
 // pass; longer rows keep a single row in flight, issued after it (Q4_K
 // two-window rows still fit two).  Deeper rings spill registers.
-template <class Fmt>
-static hipError_t launch_rows(int nwin, int wgs, int batch, int R, const float* x, const uint8_t* w, float* y,
-                              int out_feat, hipStream_t stream) {
-    if (nwin == 1) return launch(kquant_rows_kernel<Fmt, 1, 2, 1>, wgs, batch, R, x, w, y, out_feat, stream);
-    if constexpr (Fmt::kRowsMaxWindows == 2) {
-        return launch(kquant_rows_kernel<Fmt, 2, 1, 0>, wgs, batch, R, x, w, y, out_feat, stream);
+template <class Fmt, int EPI, bool MULTI, bool NORM = false>
+static hipError_t launch_rows(int nwin, int wgs, int batch, int R, const float* x, const RowsArgs& a, float* y,
+                              hipStream_t stream) {
+    const size_t lds = NORM ? norm_lds_bytes(R) : act_lds_bytes(R);
+    if (nwin == 1)
+        return launch_lds(kquant_rows_kernel<Fmt, 1, 2, 1, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a, y, R);
+    if constexpr (MULTI && Fmt::kRowsMaxWindows == 2) {
+        return hipErrorInvalidValue;  // Q6_K segment selection at two windows would spill registers
+    } else if constexpr (Fmt::kRowsMaxWindows == 2 || EPI == kEpiSwiGLU) {
+        return launch_lds(kquant_rows_kernel<Fmt, 2, 1, 0, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a, y, R);
     } else {
-        if (nwin == 2) return launch(kquant_rows_kernel<Fmt, 2, 2, 1>, wgs, batch, R, x, w, y, out_feat, stream);
-        return launch(kquant_rows_kernel<Fmt, 3, 1, 0>, wgs, batch, R, x, w, y, out_feat, stream);
+        if (nwin == 2)
+            return launch_lds(kquant_rows_kernel<Fmt, 2, 2, 1, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a, y,
+                              R);
+        return launch_lds(kquant_rows_kernel<Fmt, 3, 1, 0, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a, y, R);
     }
 }
 
@@ -573,24 +674,70 @@ static hipError_t launch_kq(const float* x, const uint8_t* w, float* y, int batc
                             int num_cus, hipStream_t stream) {
     const int R = in_feat / 256;
     const int nwin = (R + 15) / 16;
-    // one 16-wave workgroup per CU; more if a wave would own over 64 rows
-    int wgs = num_cus;
-    const int need = (out_feat + kNW * 64 - 1) / (kNW * 64);
-    if (wgs < need) wgs = need;
+    const int wgs = rows_grid(out_feat, num_cus);
     const size_t bytes = (size_t)out_feat * R * Fmt::kBytes;
-    if (nwin <= Fmt::kRowsMaxWindows && bytes < (size_t)kOutOfRange)
-        return launch_rows<Fmt>(nwin, wgs, batch, R, x, w, y, out_feat, stream);
+    if (nwin <= Fmt::kRowsMaxWindows && bytes < (size_t)kOutOfRange) {
+        const RowsArgs a{{w, w, w}, {out_feat, 0, 0}, nullptr, 0.0f};
+        return launch_rows<Fmt, kEpiStore, false>(nwin, wgs, batch, R, x, a, y, stream);
+    }
     const long waves = (long)wgs * kNW;
     const long units = ((long)out_feat + waves - 1) / waves * nwin;  // per wave, upper bound
     // 16 waves per CU leave 128 VGPRs per wave: at most 4 (Q4_K) / 2 (Q6_K) units in flight
     constexpr int kMaxD = sizeof(typename Fmt::Regs) > 48 ? 2 : 4;
-    if (units <= 1) return launch(kquant_windows_kernel<Fmt, 1>, wgs, batch, R, x, w, y, out_feat, stream);
+    if (units <= 1) return launch(kquant_windows_kernel<Fmt, 1>, wgs, batch, R, stream, x, w, y, R, out_feat);
     if constexpr (kMaxD == 2) {
-        return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, x, w, y, out_feat, stream);
+        return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, stream, x, w, y, R, out_feat);
     } else {
-        if (units <= 2) return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, x, w, y, out_feat, stream);
-        return launch(kquant_windows_kernel<Fmt, 4>, wgs, batch, R, x, w, y, out_feat, stream);
+        if (units <= 2) return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, stream, x, w, y, R, out_feat);
+        return launch(kquant_windows_kernel<Fmt, 4>, wgs, batch, R, stream, x, w, y, R, out_feat);
     }
+}
+
+bool kquant_fused_supported(int ggml_type, int in_feat, int epi, const RowsArgs& a) {
+    if ((ggml_type != 12 && ggml_type != 14) || in_feat <= 0 || in_feat % 256) return false;
+    if (epi == kEpiSwiGLU && ggml_type != 12) return false;  // Q6_K pairs would spill registers
+    const int R = in_feat / 256, nwin = (R + 15) / 16;
+    const int maxw = ggml_type == 12 ? Q4K::kRowsMaxWindows : Q6K::kRowsMaxWindows;
+    if (nwin > (epi == kEpiSwiGLU ? 2 : maxw)) return false;
+    const size_t rb = (size_t)R * (ggml_type == 12 ? Q4K::kBytes : Q6K::kBytes);
+    for (int m = 0; m < 3; m++) {
+        if (a.rows[m] < 0 || (size_t)a.rows[m] * rb >= (size_t)kOutOfRange) return false;
+        if (a.rows[m] > 0 && (reinterpret_cast<uintptr_t>(a.w[m]) & 15)) return false;
+    }
+    if (a.norm_w && (epi == kEpiAccumulate || (reinterpret_cast<uintptr_t>(a.norm_w) & 15))) return false;
+    if (epi == kEpiSwiGLU) return a.rows[0] == a.rows[1] && a.rows[2] == 0;
+    if (ggml_type == 14 && nwin > 1 && (a.rows[1] > 0 || a.rows[2] > 0)) return false;
+    return (long)a.rows[0] + a.rows[1] + a.rows[2] < (1L << 30);
+}
+
+template <class Fmt>
+static hipError_t launch_fused(int epi, const float* x, const RowsArgs& a, float* y, int R, int wgs,
+                               hipStream_t stream) {
+    const int nwin = (R + 15) / 16;
+    const bool multi = a.rows[1] > 0 || a.rows[2] > 0, norm = a.norm_w != nullptr;
+    if (epi == kEpiSwiGLU) {
+        if constexpr (std::is_same<Fmt, Q4K>::value)
+            return norm ? launch_rows<Fmt, kEpiSwiGLU, false, true>(nwin, wgs, 1, R, x, a, y, stream)
+                        : launch_rows<Fmt, kEpiSwiGLU, false>(nwin, wgs, 1, R, x, a, y, stream);
+        return hipErrorInvalidValue;
+    }
+    if (epi == kEpiAccumulate)
+        return multi ? launch_rows<Fmt, kEpiAccumulate, true>(nwin, wgs, 1, R, x, a, y, stream)
+                     : launch_rows<Fmt, kEpiAccumulate, false>(nwin, wgs, 1, R, x, a, y, stream);
+    if (norm)
+        return multi ? launch_rows<Fmt, kEpiStore, true, true>(nwin, wgs, 1, R, x, a, y, stream)
+                     : launch_rows<Fmt, kEpiStore, false, true>(nwin, wgs, 1, R, x, a, y, stream);
+    return multi ? launch_rows<Fmt, kEpiStore, true>(nwin, wgs, 1, R, x, a, y, stream)
+                 : launch_rows<Fmt, kEpiStore, false>(nwin, wgs, 1, R, x, a, y, stream);
+}
+
+hipError_t launch_kquant_fused(int ggml_type, int epi, const float* x, const RowsArgs& a, float* y, int in_feat,
+                               int num_cus, hipStream_t stream) {
+    const int out = epi == kEpiSwiGLU ? a.rows[0] : a.rows[0] + a.rows[1] + a.rows[2];
+    if (out == 0) return hipSuccess;
+    const int wgs = rows_grid(out, num_cus);
+    if (ggml_type == 12) return launch_fused<Q4K>(epi, x, a, y, in_feat / 256, wgs, stream);
+    return launch_fused<Q6K>(epi, x, a, y, in_feat / 256, wgs, stream);
 }
 
 hipError_t launch_q4k_gemv(const float* x, const uint8_t* w, float* y, int batch, int in_feat, int out_feat,

@@ -1,0 +1,80 @@
+// vtq_decode.h -- internal interface of the device-resident decode step
+// (libvtq_runtime).  All pointers are device memory; launches are
+// asynchronous on `stream`.  The position of the step being computed is read
+// from device memory (*pos), so one step's launches can be captured once in a
+// HIP graph and replayed for every position; the argmax kernel, the last of
+// the step, advances *pos.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace vtq {
+namespace decode {
+
+// This step's RoPE angles (cos, sin) per pair m < head_dim/2, written to
+// cs[2m], cs[2m+1] by the kernel that prepares the step (embed for the
+// first, argmax_advance for the next), read by attention.
+struct RopeArgs {
+    float* cs;  // nullptr: not written
+    int head_dim;
+    float theta;
+};
+
+// embedding_row (src/model/forward_quantized.rs:818-923): row tokens[*pos]
+// of the table (ggml type 0, 2, 6, 8, 12 or 14, `rows` rows) into x[0..dim);
+// a token >= rows reads row 0 instead, and the caller reports the error.
+// embed_row_bytes: bytes per table row, 0 for an unsupported type or a dim
+// that is not a whole number of blocks.
+size_t embed_row_bytes(int ggml_type, int dim);
+hipError_t embed(int ggml_type, const uint8_t* table, uint32_t rows, const uint32_t* tokens, const int* pos, int dim,
+                 float* x, const RopeArgs& rope, hipStream_t stream);
+
+// rms_norm_slice (src/ops/rms_norm.rs:60-110): out = x * scale * w with the
+// sum of squares accumulated serially, as the reference does.
+hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out, hipStream_t stream);
+
+struct AttnArgs {
+    const float* qkv;            // q[dim] | k[kv_dim] | v[kv_dim] of this step
+    const float *bq, *bk, *bv;   // optional biases (added before RoPE / the cache write)
+    float *kc, *vc;              // this layer's caches, [seq][kv_dim]
+    const float* cs;             // this step's RoPE angles (RopeArgs)
+    float* out;                  // [dim] attention output (the Wo input)
+    const int* pos;
+    int heads, kv_heads, head_dim, seq;
+    float theta;
+    int neox;                    // 1: RoPE on (j, j + head/2) pairs, 0: on (2j, 2j+1)
+};
+// RoPE of q and of this step's k, the cache write of k and v at *pos, and
+// per-head softmax attention (src/model/forward_quantized.rs:405-560).
+hipError_t attention(const AttnArgs& a, hipStream_t stream);
+
+// The embedding table, for the next step's row (see embed).
+struct EmbedArgs {
+    int type;
+    const uint8_t* table;  // nullptr: no embedding
+    uint32_t rows;
+    size_t row_bytes;
+    int dim;
+    float* x;
+    RopeArgs rope;  // the next step's angles
+};
+
+// argmax_last_dim (src/ops/argmax.rs:21-68) of logits[0..vocab): the next
+// token tokens[*pos + 1] when *pos + 1 >= prompt_len (a prompt token is
+// forced otherwise) and *pos + 1 <= total.  With hist, the logits are also
+// copied to hist[*pos * vocab ..].  Then, when *pos + 1 < total, the
+// embedding row of tokens[*pos + 1] goes to e.x (the next step's input), and
+// *pos += 1.
+hipError_t argmax_advance(const float* logits, int vocab, uint32_t* tokens, int* pos, int prompt_len, int total,
+                          float* hist, const EmbedArgs& e, hipStream_t stream);
+
+// Element-wise epilogues for linears that are not fused into the GEMV:
+// x[i] = x[i] + y[i] (residual), v[i] = v[i] + b[i] (bias),
+// out[i] = silu(gate[i]) * up[i] with silu(g) = g / (1 + expf(-g)).
+hipError_t add_inplace(float* x, const float* y, int n, hipStream_t stream);
+hipError_t swiglu(const float* gate, const float* up, float* out, int n, hipStream_t stream);
+
+}  // namespace decode
+}  // namespace vtq

@@ -1,0 +1,471 @@
+// vtq_decode.hip -- device kernels of the decode step (libvtq_runtime).
+//
+// Restates, on the device and in the reference's operation order, the parts
+// of forward_quantized::step (src/model/forward_quantized.rs:288-655) that
+// are not linears: embedding_row, rms_norm_slice, RoPE, the KV-cache write,
+// softmax attention, the residual adds, SwiGLU and argmax.  Reductions whose
+// order the reference fixes (the RMSNorm sum of squares, the softmax
+// denominator, each score's dot product, each output element's sum over
+// positions) run serially in one lane; maxima, which no order changes, run as
+// trees.  Transcendentals are the libm restatements of vtq_libm.h, so they
+// round exactly as the reference's libm crate does.
+#include "vtq_decode.h"
+#include "vtq_device.h"
+#include "vtq_libm.h"
+
+namespace vtq {
+namespace decode {
+
+namespace {
+
+__device__ __forceinline__ uint32_t rd_u16(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+// one element of the table row (dequantize_* of src/ops/quant.rs)
+__device__ float embed_elem(int type, const uint8_t* row, int i) {
+    switch (type) {
+    case 0:
+        return reinterpret_cast<const float*>(row)[i];
+    case 2: {  // dequantize_q4_0: element 2k low nibble, 2k+1 high
+        const uint8_t* blk = row + 18 * (i / 32);
+        const int e = i % 32, k = e / 2;
+        const int q = (int)((blk[2 + k] >> (4 * (e & 1))) & 15) - 8;
+        return f16_to_f32_sel(rd_u16(blk)) * (float)q;
+    }
+    case 6: {  // dequantize_q5_0: element j and j+16 share qs byte j
+        const uint8_t* blk = row + 22 * (i / 32);
+        const int e = i % 32;
+        const uint32_t qh = (uint32_t)blk[2] | ((uint32_t)blk[3] << 8) | ((uint32_t)blk[4] << 16) |
+                            ((uint32_t)blk[5] << 24);
+        int x;
+        if (e < 16)
+            x = (int)((blk[6 + e] & 15) | (((qh >> e) << 4) & 16)) - 16;
+        else
+            x = (int)((blk[6 + e - 16] >> 4) | ((qh >> (e - 16 + 12)) & 16)) - 16;
+        return f16_to_f32_sel(rd_u16(blk)) * (float)x;
+    }
+    case 8: {  // dequantize_q8_0
+        const uint8_t* blk = row + 34 * (i / 32);
+        return f16_to_f32_sel(rd_u16(blk)) * (float)(int8_t)blk[2 + i % 32];
+    }
+    case 12: {  // dequantize_q4_k: d1 * q - m1 per 32-element sub-block
+        const uint8_t* blk = row + 144 * (i / 256);
+        const int e = i % 256, j = e / 32, l = e % 32;
+        const uint8_t* s = blk + 4;
+        uint32_t sc, mn;
+        if (j < 4) {
+            sc = s[j] & 63;
+            mn = s[j + 4] & 63;
+        } else {
+            sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+            mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+        }
+        const float d1 = f16_to_f32_sel(rd_u16(blk)) * (float)sc;
+        const float m1 = f16_to_f32_sel(rd_u16(blk + 2)) * (float)mn;
+        const uint8_t qb = blk[16 + 32 * (j / 2) + l];
+        const uint32_t q = (j & 1) ? (qb >> 4) : (qb & 15);
+        return d1 * (float)q - m1;
+    }
+    default: {  // 14, dequantize_q6_k: (d * sc) * q, q = 6-bit code - 32
+        const uint8_t* blk = row + 210 * (i / 256);
+        const int e = i % 256, hf = e / 128, r = e % 128, k = r / 32, l = r % 32;
+        const uint8_t* ql = blk + 64 * hf;
+        const uint8_t h = blk[128 + 32 * hf + l];
+        const uint8_t lo = ql[l + 32 * (k & 1)];
+        const int q = (int)(((k >= 2) ? (lo >> 4) : (lo & 15)) | (((h >> (2 * k)) & 3) << 4)) - 32;
+        const float d = f16_to_f32_sel(rd_u16(blk + 208));
+        return d * (float)(int8_t)blk[192 + 8 * hf + l / 16 + 2 * k] * (float)q;
+    }
+    }
+}
+
+size_t row_bytes(int type, int dim) {
+    switch (type) {
+    case 0: return (size_t)dim * 4;
+    case 2: return (size_t)dim / 32 * 18;
+    case 6: return (size_t)dim / 32 * 22;
+    case 8: return (size_t)dim / 32 * 34;
+    case 12: return (size_t)dim / 256 * 144;
+    default: return (size_t)dim / 256 * 210;
+    }
+}
+
+// RoPE angles of position q for pair m = 0..head_dim/2 - 1
+// (forward_quantized.rs:417-456): e = (2m)/head_dim, freq = 1 / theta^e,
+// val = q * freq; cs[2m] = cos(val), cs[2m+1] = sin(val).  The same for
+// every head and layer, so computed once per step.
+__device__ void rope_table(const RopeArgs& r, int q) {
+    for (int m = threadIdx.x; m < r.head_dim / 2; m += blockDim.x) {
+        const float e = (float)(2 * m) / (float)r.head_dim;
+        const float freq = 1.0f / libm::powf(r.theta, e);
+        const float val = (float)q * freq;
+        r.cs[2 * m] = libm::cosf(val);
+        r.cs[2 * m + 1] = libm::sinf(val);
+    }
+}
+
+// a token past the table reads row 0 (the host reports the reference's error)
+__global__ __launch_bounds__(256) void embed_kernel(int type, const uint8_t* __restrict__ table, uint32_t rows,
+                                                    const uint32_t* __restrict__ tokens, const int* __restrict__ pos,
+                                                    int dim, size_t rb, float* __restrict__ x, RopeArgs rope) {
+    if (rope.cs) rope_table(rope, *pos);
+    const uint32_t tok = tokens[*pos];
+    const uint8_t* row = table + (size_t)(tok < rows ? tok : 0u) * rb;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) x[i] = embed_elem(type, row, i);
+}
+
+// products in parallel, the sum of squares serially in one lane
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int n,
+                                                       float eps, float* __restrict__ out) {
+    extern __shared__ float4 prod4[];
+    float* prod = reinterpret_cast<float*>(prod4);
+    __shared__ float scale_s;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) prod[i] = x[i] * x[i];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const float sumsq = serial_sum_lds(prod, n);
+        const float mean = sumsq / (float)n;
+        scale_s = 1.0f / libm::sqrtf(mean + eps);
+    }
+    __syncthreads();
+    const float scale = scale_s;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * scale * w[i];
+}
+
+constexpr int kAttnThreads = 256;
+constexpr int kAttnTile = 256;  // cached v positions per LDS tile at head_dim 64 (64 KiB)
+
+// max in the reference's sense (strict >, NaN never wins), as a tree
+__device__ float block_max(float m, float* red) {
+    red[threadIdx.x] = m;
+    __syncthreads();
+    for (int s = kAttnThreads / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            const float o = red[threadIdx.x + s];
+            if (o > red[threadIdx.x]) red[threadIdx.x] = o;
+        }
+        __syncthreads();
+    }
+    const float r = red[0];
+    __syncthreads();
+    return r;
+}
+
+// One workgroup per query head h.  Shared: q (roped), this step's k (roped)
+// and v of h's KV head, then the attention weights of positions 0..pos.
+// HD > 0: the head dimension as a compile-time constant; with HD == 64 and
+// pos < kAttnThreads every global load of the kernel (q, k, v, the rope
+// angles, thread t's cached k row, the cached v rows) is issued at once.
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
+    extern __shared__ float4 sh4[];
+    float* sh = reinterpret_cast<float*>(sh4);
+    const int hd = HD > 0 ? HD : a.head_dim, h = blockIdx.x, kv_mul = a.heads / a.kv_heads, hk = h / kv_mul;
+    const int kv_dim = a.kv_heads * hd, dim = a.heads * hd;
+    float* qs = sh;
+    float* kp = qs + hd;
+    float* vp = kp + hd;
+    float* red = vp + hd;
+    float* att = red + kAttnThreads + (4 - (3 * hd) % 4) % 4;  // 16-byte aligned for float4 reads
+    float* vt = att + ((a.seq + 3) & ~3);
+    const int p = *a.pos;
+    const int t0 = threadIdx.x;
+    constexpr bool kFast = HD == 64;
+    const bool fast = kFast && p < kAttnThreads;
+    // q, k, v (+ bias, forward_quantized.rs:390-404), then (fast path) thread
+    // t's cached k row into registers and the cached v rows into LDS: every
+    // load is issued before the first one is waited for
+    float qv = 0.0f, kv = 0.0f, vv = 0.0f;
+    if (t0 < hd) qv = a.qkv[h * hd + t0], kv = a.qkv[dim + hk * hd + t0], vv = a.qkv[dim + kv_dim + hk * hd + t0];
+    constexpr int KPT = kFast ? HD / 4 : 1;
+    float4 kr[KPT];
+    if constexpr (kFast) {
+        // rows >= pos are never used: clamped to row 0, always in bounds
+        const float4* krow = reinterpret_cast<const float4*>(a.kc + (size_t)(t0 < p ? t0 : 0) * kv_dim + hk * hd);
+#pragma unroll
+        for (int j = 0; j < KPT; j++) kr[j] = krow[j];
+        if (fast) {
+            // all kAttnThreads * HD/4 float4 of the tile; rows >= pos hold
+            // copies of row 0 and are never read
+#pragma unroll
+            for (int u = 0; u < HD / 4; u++) {
+                const int i = t0 + kAttnThreads * u, t = i / (HD / 4);
+                reinterpret_cast<float4*>(vt)[i] =
+                    reinterpret_cast<const float4*>(a.vc + (size_t)(t < p ? t : 0) * kv_dim + hk * hd)[i % (HD / 4)];
+            }
+        }
+    }
+    for (int d = t0; d < hd; d += kAttnThreads) {
+        float q = d == t0 ? qv : a.qkv[h * hd + d], k = d == t0 ? kv : a.qkv[dim + hk * hd + d],
+              v = d == t0 ? vv : a.qkv[dim + kv_dim + hk * hd + d];
+        if (a.bq) q = q + a.bq[h * hd + d];
+        if (a.bk) k = k + a.bk[hk * hd + d];
+        if (a.bv) v = v + a.bv[hk * hd + d];
+        qs[d] = q;
+        kp[d] = k;
+        vp[d] = v;
+    }
+    __syncthreads();
+    // RoPE with this step's angles (rope_table)
+    for (int m = t0; m < hd / 2; m += kAttnThreads) {
+        const float c = a.cs[2 * m], s = a.cs[2 * m + 1];
+        const int i0 = a.neox ? m : 2 * m, i1 = a.neox ? m + hd / 2 : 2 * m + 1;
+        const float q0 = qs[i0], q1 = qs[i1], k0 = kp[i0], k1 = kp[i1];
+        qs[i0] = q0 * c - q1 * s;
+        qs[i1] = q0 * s + q1 * c;
+        kp[i0] = k0 * c - k1 * s;
+        kp[i1] = k0 * s + k1 * c;
+    }
+    __syncthreads();
+    // the cache write, once per KV head; other heads of the group read
+    // positions < pos from the cache and this position from kp / vp
+    if (h % kv_mul == 0) {
+        for (int d = t0; d < hd; d += kAttnThreads) {
+            a.kc[(size_t)p * kv_dim + hk * hd + d] = kp[d];
+            a.vc[(size_t)p * kv_dim + hk * hd + d] = vp[d];
+        }
+    }
+    // scores: sum over d in order, then / sqrt(head_dim)
+    const float sq = libm::sqrtf((float)hd);
+    float mx = -__builtin_inff();
+    if (fast) {
+        if (t0 <= p) {
+            float score = 0.0f;
+            if (t0 < p) {
+#pragma unroll
+                for (int j = 0; j < KPT; j++) {
+                    const float4 q4 = reinterpret_cast<const float4*>(qs)[j];
+                    score += q4.x * kr[j].x;
+                    score += q4.y * kr[j].y;
+                    score += q4.z * kr[j].z;
+                    score += q4.w * kr[j].w;
+                }
+            } else {
+                for (int d = 0; d < hd; d++) score += qs[d] * kp[d];
+            }
+            score /= sq;
+            att[t0] = score;
+            mx = score;
+        }
+    } else {
+        for (int t = t0; t <= p; t += kAttnThreads) {
+            const float* kt = t == p ? kp : a.kc + (size_t)t * kv_dim + hk * hd;
+            float score = 0.0f;
+            for (int d = 0; d < hd; d++) score += qs[d] * kt[d];
+            score /= sq;
+            att[t] = score;
+            if (score > mx) mx = score;
+        }
+    }
+    // softmax_inplace (forward_quantized.rs:925-941)
+    mx = block_max(mx, red);
+    for (int t = t0; t <= p; t += kAttnThreads) att[t] = libm::expf(att[t] - mx);
+    __syncthreads();
+    if (t0 == 0) red[0] = 1.0f / serial_sum_lds(att, p + 1);
+    __syncthreads();
+    const float inv = red[0];
+    for (int t = t0; t <= p; t += kAttnThreads) att[t] *= inv;
+    // out[d] = sum over t in order of att[t] * v_t[d]: the cached v rows go
+    // through LDS (in tiles of kAttnTile * 64 floats unless the fast path
+    // already holds them all in registers), this position's v comes from vp
+    auto accumulate = [&](float& acc, int c0, int nt) {
+        if (t0 < hd) {
+            int t = 0;
+            for (; t + 8 <= nt; t += 8) {
+                float vb[8], ab[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    vb[j] = vt[(t + j) * hd + t0];
+                    ab[j] = att[c0 + t + j];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc += ab[j] * vb[j];
+            }
+            for (; t < nt; t++) acc += att[c0 + t] * vt[t * hd + t0];
+        }
+    };
+    float acc = 0.0f;
+    if (fast) {
+        __syncthreads();
+        accumulate(acc, 0, p);
+    } else {
+        const int tile = kAttnTile * 64 / hd;
+        for (int c0 = 0; c0 < p; c0 += tile) {
+            const int nt = p - c0 < tile ? p - c0 : tile;
+            for (int i = t0; i < nt * hd / 4; i += kAttnThreads) {
+                const int t = i / (hd / 4), q4 = i % (hd / 4);
+                reinterpret_cast<float4*>(vt)[i] =
+                    *reinterpret_cast<const float4*>(a.vc + (size_t)(c0 + t) * kv_dim + hk * hd + 4 * q4);
+            }
+            __syncthreads();
+            accumulate(acc, c0, nt);
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+    if (t0 < hd) a.out[h * hd + t0] = acc + att[p] * vp[t0];
+}
+
+constexpr int kArgThreads = 1024;
+
+// argmax of step p, then the embedding row of the token step p+1 consumes
+// (the prompt's while p+1 < prompt_len, the pick after), into x
+__global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __restrict__ v, int n,
+                                                             uint32_t* __restrict__ tokens, int* __restrict__ pos,
+                                                             int prompt_len, int total, float* __restrict__ hist,
+                                                             EmbedArgs e) {
+    __shared__ float bv[kArgThreads];
+    __shared__ int bi[kArgThreads];
+    __shared__ uint32_t next_s;
+    const int p = *pos;
+    // first index of the largest non-NaN value (strict > in index order);
+    // thread t scans float4 groups t, t + kArgThreads, ... in index order
+    float b = 0.0f;
+    int idx = -1;
+    const int n4 = n / 4;
+    constexpr int U = 8;
+    for (int g0 = threadIdx.x; g0 < n4; g0 += U * kArgThreads) {
+        float4 r[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int g = g0 + u * kArgThreads;
+            r[u] = reinterpret_cast<const float4*>(v)[g < n4 ? g : 0];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int g = g0 + u * kArgThreads;
+            if (g < n4) {
+                const float xs[4] = {r[u].x, r[u].y, r[u].z, r[u].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (xs[k] == xs[k] && (idx < 0 || xs[k] > b)) {
+                        b = xs[k];
+                        idx = 4 * g + k;
+                    }
+                if (hist) reinterpret_cast<float4*>(hist + (size_t)p * n)[g] = r[u];
+            }
+        }
+    }
+    for (int i = 4 * n4 + threadIdx.x; i < n; i += kArgThreads) {
+        const float x = v[i];
+        if (hist) hist[(size_t)p * n + i] = x;
+        if (x == x && (idx < 0 || x > b)) {
+            b = x;
+            idx = i;
+        }
+    }
+    bv[threadIdx.x] = b;
+    bi[threadIdx.x] = idx;
+    __syncthreads();
+    for (int s = kArgThreads / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            const int oi = bi[threadIdx.x + s], mi = bi[threadIdx.x];
+            const float ov = bv[threadIdx.x + s], mv = bv[threadIdx.x];
+            if (oi >= 0 && (mi < 0 || ov > mv || (ov == mv && oi < mi))) {
+                bv[threadIdx.x] = ov;
+                bi[threadIdx.x] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        // a NaN at index 0 is never beaten (argmax.rs: strict > against it)
+        const uint32_t best = (v[0] != v[0] || bi[0] < 0) ? 0u : (uint32_t)bi[0];
+        uint32_t next = best;
+        if (p + 1 >= prompt_len && p + 1 <= total)
+            tokens[p + 1] = best;
+        else if (p + 1 < prompt_len)
+            next = tokens[p + 1];
+        next_s = next;
+        *pos = p + 1;
+    }
+    __syncthreads();
+    if (p + 1 < total && e.rope.cs) rope_table(e.rope, p + 1);
+    if (p + 1 < total && e.table) {
+        const uint32_t tok = next_s;
+        const uint8_t* row = e.table + (size_t)(tok < e.rows ? tok : 0u) * e.row_bytes;
+        for (int i = threadIdx.x; i < e.dim; i += kArgThreads) e.x[i] = embed_elem(e.type, row, i);
+    }
+}
+
+__global__ void add_kernel(float* __restrict__ x, const float* __restrict__ y, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = x[i] + y[i];
+}
+
+__global__ void swiglu_kernel(const float* __restrict__ gate, const float* __restrict__ up, float* __restrict__ out,
+                              int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float g = gate[i];
+        const float silu = g / (1.0f + libm::expf(-g));
+        out[i] = silu * up[i];
+    }
+}
+
+}  // namespace
+
+size_t embed_row_bytes(int ggml_type, int dim) {
+    switch (ggml_type) {
+    case 0: case 2: case 6: case 8: case 12: case 14: break;
+    default: return 0;
+    }
+    const int blk = (ggml_type == 12 || ggml_type == 14) ? 256 : ggml_type == 0 ? 1 : 32;
+    return dim > 0 && dim % blk == 0 ? row_bytes(ggml_type, dim) : 0;
+}
+
+hipError_t embed(int ggml_type, const uint8_t* table, uint32_t rows, const uint32_t* tokens, const int* pos, int dim,
+                 float* x, const RopeArgs& rope, hipStream_t stream) {
+    hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, stream, ggml_type, table, rows, tokens, pos, dim,
+                       row_bytes(ggml_type, dim), x, rope);
+    return hipGetLastError();
+}
+
+hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out, hipStream_t stream) {
+    const size_t lds = (size_t)n * 4;
+    if (lds > 65536) {
+        if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(rms_norm_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds))
+            return e;
+    }
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(256), lds, stream, x, w, n, eps, out);
+    return hipGetLastError();
+}
+
+template <int HD>
+static hipError_t launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
+    if (lds > 65536) {
+        if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<HD>),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds))
+            return e;
+    }
+    hipLaunchKernelGGL(attention_kernel<HD>, dim3((unsigned)a.heads), dim3(kAttnThreads), lds, stream, a);
+    return hipGetLastError();
+}
+
+hipError_t attention(const AttnArgs& a, hipStream_t stream) {
+    if (a.head_dim > kAttnThreads || a.head_dim % 4 || (kAttnTile * 64) % a.head_dim) return hipErrorInvalidValue;
+    const size_t lds = ((size_t)3 * a.head_dim + kAttnThreads + 4 + ((a.seq + 3) & ~3) + kAttnTile * 64) * 4;
+    if (a.head_dim == 64) return launch_attention<64>(a, lds, stream);
+    if (a.head_dim == 128) return launch_attention<128>(a, lds, stream);
+    return launch_attention<0>(a, lds, stream);
+}
+
+hipError_t argmax_advance(const float* logits, int vocab, uint32_t* tokens, int* pos, int prompt_len, int total,
+                          float* hist, const EmbedArgs& e, hipStream_t stream) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgThreads), 0, stream, logits, vocab, tokens, pos, prompt_len,
+                       total, hist, e);
+    return hipGetLastError();
+}
+
+hipError_t add_inplace(float* x, const float* y, int n, hipStream_t stream) {
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t swiglu(const float* gate, const float* up, float* out, int n, hipStream_t stream) {
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, gate, up, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace decode
+}  // namespace vtq

@@ -22,6 +22,24 @@ hipError_t launch_q6k_gemv(const float* x, const uint8_t* w, float* y, int batch
                            int num_cus, hipStream_t stream);
 hipError_t launch_canon_gemv(CanonFormat fmt, const float* x, const uint8_t* w, size_t row_bytes, float* y,
                              int batch, int in_feat, int out_feat, int num_cus, hipStream_t stream);
+// Decode-step GEMV (integer regime, Q4_K = 12 / Q6_K = 14, batch 1): the
+// output rows are the concatenation of up to three matrices that share x
+// (unused slots have rows 0).  Epilogues: store, accumulate into y (the
+// residual add), or SwiGLU of two equal-row matrices (y[i] = silu(g_i)*u_i).
+// With norm_w set (store and SwiGLU only), x is first replaced by
+// rms_norm(x, norm_w, eps) (src/ops/rms_norm.rs:60-110), computed by every
+// workgroup from the raw x.
+enum RowsEpilogue { kEpiStore = 0, kEpiAccumulate = 1, kEpiSwiGLU = 2 };
+struct RowsArgs {
+    const uint8_t* w[3];
+    int rows[3];
+    const float* norm_w = nullptr;
+    float eps = 0.0f;
+};
+bool kquant_fused_supported(int ggml_type, int in_feat, int epi, const RowsArgs& a);
+hipError_t launch_kquant_fused(int ggml_type, int epi, const float* x, const RowsArgs& a, float* y, int in_feat,
+                               int num_cus, hipStream_t stream);
+
 hipError_t launch_fill(float* y, size_t n, float v, hipStream_t stream);
 
 // Prefill GEMM (batch >= kGemmMinBatch): activation pre-pass into `workspace`

@@ -1,5 +1,6 @@
-// vtq_runtime.hip -- libvtq_runtime: the reference's quantized decode with
-// every linear layer on the GPU through libvtq (include/vtq_runtime.h).
+// vtq_runtime.hip -- libvtq_runtime: the reference's quantized decode,
+// device-resident, with every linear on the GPU through libvtq
+// (include/vtq_runtime.h).
 //
 // Restates, in the reference's operation order:
 //   GgufFile::parse          src/model/gguf.rs:305-421
@@ -12,31 +13,29 @@
 //   argmax_last_dim          src/ops/argmax.rs:21-68
 //   run_quantized            src/model/inference.rs:274-345
 //   compute_digest (v2)      src/cert/builder.rs:458-597
-// The GGUF blob is uploaded once; linears read their weights in place on the
-// device.  Host work per step: embedding row, RMSNorm, RoPE, attention over
-// the KV cache (heads spread over a thread pool; each head's arithmetic is
-// sequential exactly as in the reference), SwiGLU, residuals, argmax.
+// The GGUF blob is uploaded once; the activations, the KV cache, the token
+// sequence and the step position live in device memory, so a decode step is
+// a fixed sequence of kernel launches (vtq_decode.hip for the non-linear
+// parts, libvtq for the linears) that is captured once per run in a HIP graph
+// and replayed for every position.  The host only uploads the prompt and
+// reads back the generated tokens (and the logits history, when asked for)
+// once at the end.  In the integer regime the Q4_K / Q6_K linears of a layer
+// are fused: q, k and v in one launch, the residual add into the Wo and W2
+// launches, SwiGLU into the W1 / W3 launch.
 #include <hip/hip_runtime.h>
 
-#include <atomic>
-#include <condition_variable>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <functional>
 #include <algorithm>
 #include <map>
-#include <memory>
-#include <mutex>
 #include <string>
-#include <thread>
 #include <vector>
 
 #include "../../include/vtq.h"
 #include "../../include/vtq_runtime.h"
-#include "vtq_libm.h"
-
-namespace libm = vtq::libm;
+#include "vtq_decode.h"
+#include "vtq_kernels.h"
 
 namespace {
 
@@ -169,71 +168,6 @@ void leb128(Blake3& h, uint64_t v) {
     h.update(b, (size_t)n);
 }
 
-// ---------------------------------------------------------------- thread pool
-class Pool {
-  public:
-    explicit Pool(int n) {
-        for (int i = 0; i < n; i++) workers_.emplace_back([this, i] { run(i); });
-    }
-    ~Pool() {
-        {
-            std::lock_guard<std::mutex> l(mu_);
-            stop_ = true;
-        }
-        cv_.notify_all();
-        for (auto& t : workers_) t.join();
-    }
-    int size() const { return (int)workers_.size() + 1; }
-    // fn(i) for i in [0, n): items are independent, so the split is free
-    void parallel_for(int n, const std::function<void(int)>& fn) {
-        if (workers_.empty() || n <= 1) {
-            for (int i = 0; i < n; i++) fn(i);
-            return;
-        }
-        {
-            std::lock_guard<std::mutex> l(mu_);
-            fn_ = &fn;
-            n_ = n;
-            next_.store(0);
-            pending_ = (int)workers_.size();
-            gen_++;
-        }
-        cv_.notify_all();
-        for (int i; (i = next_.fetch_add(1)) < n;) fn(i);
-        std::unique_lock<std::mutex> l(mu_);
-        done_.wait(l, [this] { return pending_ == 0; });
-        fn_ = nullptr;
-    }
-
-  private:
-    void run(int) {
-        uint64_t seen = 0;
-        for (;;) {
-            const std::function<void(int)>* fn;
-            int n;
-            {
-                std::unique_lock<std::mutex> l(mu_);
-                cv_.wait(l, [&] { return stop_ || gen_ != seen; });
-                if (stop_) return;
-                seen = gen_;
-                fn = fn_;
-                n = n_;
-            }
-            for (int i; (i = next_.fetch_add(1)) < n;) (*fn)(i);
-            std::lock_guard<std::mutex> l(mu_);
-            if (--pending_ == 0) done_.notify_one();
-        }
-    }
-    std::vector<std::thread> workers_;
-    std::mutex mu_;
-    std::condition_variable cv_, done_;
-    const std::function<void(int)>* fn_ = nullptr;
-    int n_ = 0, pending_ = 0;
-    std::atomic<int> next_{0};
-    uint64_t gen_ = 0;
-    bool stop_ = false;
-};
-
 // ---------------------------------------------------------------- GGUF
 struct Tensor {
     uint32_t type = 0;
@@ -313,48 +247,38 @@ bool tensor_bytes(uint32_t type, uint64_t numel, size_t* out) {
 }
 
 // exact f16 -> f32 (src/ops/quant.rs:40-66)
-float f16(const uint8_t* p) {
-    const uint32_t h = (uint32_t)p[0] | ((uint32_t)p[1] << 8);
-    const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1f, m = h & 0x3ff;
-    uint32_t bits;
-    if (e == 0) {
-        const float v = (float)m * 0x1p-24f;
-        bits = __builtin_bit_cast(uint32_t, v) | sign;
-    } else if (e == 31) {
-        bits = sign | 0x7f800000u | (m << 13);
-    } else {
-        bits = sign | ((e + 112) << 23) | (m << 13);
-    }
-    return __builtin_bit_cast(float, bits);
-}
-
 struct Lin {
     int type = 0;
     size_t offset = 0, nbytes = 0;
 };
 
 struct Layer {
-    const float *rms_att = nullptr, *rms_ffn = nullptr, *bq = nullptr, *bk = nullptr, *bv = nullptr;
+    size_t rms_att = 0, rms_ffn = 0, bq = 0, bk = 0, bv = 0;  // blob offsets of F32 tensors (0: absent)
     Lin wq, wk, wv, wo, w1, w2, w3;
 };
 
 }  // namespace
 
 struct vtqrt_model {
-    std::vector<uint8_t> blob;  // host copy (norms, embedding rows)
-    uint8_t* dblob = nullptr;   // device copy (linear weights)
+    std::vector<uint8_t> blob;  // host copy (metadata, shapes)
+    uint8_t* dblob = nullptr;   // device copy: every tensor is read in place
     vtq_ctx* ctx = nullptr;
     hipStream_t stream = nullptr;
     std::string err;
+    int device = 0, num_cus = 0;
     int dim = 0, hidden = 0, layers = 0, heads = 0, kv_heads = 0, vocab = 0, seq = 0;
     bool shared = false, neox = false;
     float theta = 10000.0f, eps = 1e-5f;
     Lin tok, wcls;
-    const float* rms_final = nullptr;
+    size_t rms_final = 0;  // blob offsets of F32 tensors
     std::vector<Layer> L;
-    // device activations and pinned host staging
-    float *dx = nullptr, *dy = nullptr, *hx = nullptr, *hy = nullptr;
-    std::unique_ptr<Pool> pool;
+    // device state of a run: activations, KV cache, tokens, position
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr, *gate = nullptr,
+          *up = nullptr, *tmp = nullptr, *logits = nullptr, *kc = nullptr, *vc = nullptr, *hist = nullptr,
+          *rope = nullptr;
+    size_t hist_cap = 0;
+    uint32_t* tokens = nullptr;
+    int* pos = nullptr;
 };
 
 namespace {
@@ -369,251 +293,138 @@ int hip_check(vtqrt_model* m, hipError_t e, const char* where) {
     return fail(m, VTQ_E_GPU, std::string("GpuError: ") + where + ": " + hipGetErrorString(e));
 }
 
-// ---- one linear on the device: x (host) -> y (host), several outputs of
-// the same input share one upload and one synchronisation.
-struct LinCall {
-    const Lin* w;
-    int out_feat;
-    float* y;
-};
-
-int linears(vtqrt_model* m, int regime, const float* x, int in_feat, std::initializer_list<LinCall> calls) {
-    std::memcpy(m->hx, x, (size_t)in_feat * 4);
-    int rc = hip_check(m, hipMemcpyAsync(m->dx, m->hx, (size_t)in_feat * 4, hipMemcpyHostToDevice, m->stream),
-                       "hipMemcpyAsync(x)");
-    if (rc) return rc;
-    size_t off = 0;
-    for (const LinCall& c : calls) {
-        rc = vtq_linear_device(m->ctx, c.w->type, regime, m->dx, m->dblob + c.w->offset, c.w->nbytes, m->dy + off,
-                               1, (size_t)in_feat, (size_t)c.out_feat, m->stream);
-        if (rc) return fail(m, rc, vtq_last_error(m->ctx));
-        off += ((size_t)c.out_feat + 63) / 64 * 64;
-    }
-    rc = hip_check(m, hipMemcpyAsync(m->hy, m->dy, off * 4, hipMemcpyDeviceToHost, m->stream), "hipMemcpyAsync(y)");
-    if (rc) return rc;
-    rc = hip_check(m, hipStreamSynchronize(m->stream), "hipStreamSynchronize");
-    if (rc) return rc;
-    off = 0;
-    for (const LinCall& c : calls) {
-        std::memcpy(c.y, m->hy + off, (size_t)c.out_feat * 4);
-        off += ((size_t)c.out_feat + 63) / 64 * 64;
-    }
-    return VTQ_OK;
+const float* f32_at(const vtqrt_model* m, size_t off) {
+    return off ? reinterpret_cast<const float*>(m->dblob + off) : nullptr;
 }
 
-void rms_norm(const float* x, const float* w, int n, float eps, float* out) {
-    float sumsq = 0.0f;
-    for (int i = 0; i < n; i++) sumsq += x[i] * x[i];
-    const float mean = sumsq / (float)n;
-    const float scale = 1.0f / libm::sqrtf(mean + eps);
-    for (int i = 0; i < n; i++) out[i] = x[i] * scale * w[i];
+// y = W x through the C ABI (any type, either regime)
+int linear(vtqrt_model* m, int regime, const Lin& w, const float* x, int in_feat, int out_feat, float* y) {
+    const int rc = vtq_linear_device(m->ctx, w.type, regime, x, m->dblob + w.offset, w.nbytes, y, 1, (size_t)in_feat,
+                                     (size_t)out_feat, m->stream);
+    return rc ? fail(m, rc, vtq_last_error(m->ctx)) : VTQ_OK;
 }
 
-int embedding_row(vtqrt_model* m, int row, float* out) {
-    const Lin& t = m->tok;
-    const int dim = m->dim;
-    const uint8_t* base = m->blob.data() + t.offset;
-    size_t rb;
-    switch (t.type) {
-    case 0: rb = (size_t)dim * 4; break;
-    case 2: rb = (size_t)dim / 32 * 18; break;
-    case 6: rb = (size_t)dim / 32 * 22; break;
-    case 8: rb = (size_t)dim / 32 * 34; break;
-    case 12: rb = (size_t)dim / 256 * 144; break;
-    case 14: rb = (size_t)dim / 256 * 210; break;
-    default: return fail(m, VTQ_E_NOT_IMPLEMENTED, "embedding_row: non-Q4_0 / Q4_K / Q6_K / Q8_0 / F32 embedding dtype");
-    }
-    if ((size_t)(row + 1) * rb > t.nbytes) return fail(m, VTQ_E_INTERNAL, "embedding_row: row past end of table");
-    const uint8_t* r = base + (size_t)row * rb;
-    switch (t.type) {
-    case 0:
-        std::memcpy(out, r, rb);
-        break;
-    case 2:  // dequantize_q4_0: element 2k low nibble, 2k+1 high
-        for (int b = 0; b < dim / 32; b++) {
-            const uint8_t* blk = r + 18 * b;
-            const float d = f16(blk);
-            for (int k = 0; k < 16; k++) {
-                out[32 * b + 2 * k] = d * (float)((int)(blk[2 + k] & 15) - 8);
-                out[32 * b + 2 * k + 1] = d * (float)((int)(blk[2 + k] >> 4) - 8);
-            }
-        }
-        break;
-    case 6:  // dequantize_q5_0: element j and j+16 share qs byte j
-        for (int b = 0; b < dim / 32; b++) {
-            const uint8_t* blk = r + 22 * b;
-            const float d = f16(blk);
-            uint32_t qh;
-            std::memcpy(&qh, blk + 2, 4);
-            for (int j = 0; j < 16; j++) {
-                const int x0 = (int)((blk[6 + j] & 15) | (((qh >> j) << 4) & 16)) - 16;
-                const int x1 = (int)((blk[6 + j] >> 4) | ((qh >> (j + 12)) & 16)) - 16;
-                out[32 * b + j] = d * (float)x0;
-                out[32 * b + j + 16] = d * (float)x1;
-            }
-        }
-        break;
-    case 8:  // dequantize_q8_0
-        for (int b = 0; b < dim / 32; b++) {
-            const uint8_t* blk = r + 34 * b;
-            const float d = f16(blk);
-            for (int k = 0; k < 32; k++) out[32 * b + k] = d * (float)(int8_t)blk[2 + k];
-        }
-        break;
-    case 12:  // dequantize_q4_k: d1*q - m1 per 32-element sub-block
-        for (int b = 0; b < dim / 256; b++) {
-            const uint8_t* blk = r + 144 * b;
-            const float d = f16(blk), dmin = f16(blk + 2);
-            const uint8_t* s = blk + 4;
-            for (int j = 0; j < 8; j++) {
-                uint32_t sc, mn;
-                if (j < 4) {
-                    sc = s[j] & 63;
-                    mn = s[j + 4] & 63;
-                } else {
-                    sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
-                    mn = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
-                }
-                const float d1 = d * (float)sc, m1 = dmin * (float)mn;
-                const uint8_t* qs = blk + 16 + 32 * (j / 2);
-                for (int l = 0; l < 32; l++) {
-                    const uint32_t q = (j & 1) ? (qs[l] >> 4) : (qs[l] & 15);
-                    out[256 * b + 32 * j + l] = d1 * (float)q - m1;
-                }
-            }
-        }
-        break;
-    case 14:  // dequantize_q6_k: d * sc * q, q = 6-bit code - 32
-        for (int b = 0; b < dim / 256; b++) {
-            const uint8_t* blk = r + 210 * b;
-            const float d = f16(blk + 208);
-            for (int hf = 0; hf < 2; hf++) {
-                const uint8_t *ql = blk + 64 * hf, *qh = blk + 128 + 32 * hf, *sc = blk + 192 + 8 * hf;
-                float* o = out + 256 * b + 128 * hf;
-                for (int l = 0; l < 32; l++) {
-                    const int is = l / 16;
-                    const uint8_t h = qh[l];
-                    const int q[4] = {(int)((ql[l] & 15) | ((h & 3) << 4)) - 32,
-                                      (int)((ql[l + 32] & 15) | (((h >> 2) & 3) << 4)) - 32,
-                                      (int)((ql[l] >> 4) | (((h >> 4) & 3) << 4)) - 32,
-                                      (int)((ql[l + 32] >> 4) | (((h >> 6) & 3) << 4)) - 32};
-                    for (int k = 0; k < 4; k++) o[l + 32 * k] = d * (float)(int8_t)sc[is + 2 * k] * (float)q[k];
-                }
-            }
-        }
-        break;
-    }
-    return VTQ_OK;
+// rows of the embedding table (embedding_row checks a row against the table's bytes)
+uint32_t table_rows(const vtqrt_model* m) {
+    const size_t rb = vtq::decode::embed_row_bytes(m->tok.type, m->dim);
+    return rb ? (uint32_t)std::min<size_t>(m->tok.nbytes / rb, 0xFFFFFFFFu) : 0u;
 }
 
-struct State {
-    std::vector<float> kc, vc, x, xb, q, k, v, xo, x2, gate, up, ffn, logits, cosv, sinv, att;
-};
-
-int step(vtqrt_model* m, State& s, int regime, uint32_t token, int pos) {
-    const int dim = m->dim, head = dim / m->heads, kv_dim = m->kv_heads * head, kv_mul = m->heads / m->kv_heads;
-    const int hidden = m->hidden;
-    int rc = embedding_row(m, (int)token, s.x.data());
-    if (rc) return rc;
-    // RoPE angles depend only on (pos, index): computed once per step with
-    // the reference's expressions (forward_quantized.rs:417-456)
-    const int nrot = m->neox ? head / 2 : dim / 2;
-    for (int i = 0; i < nrot; i++) {
-        const float e = m->neox ? (float)(2 * i) / (float)head : (float)((2 * i) % head) / (float)head;
-        const float freq = 1.0f / libm::powf(m->theta, e);
-        const float val = (float)pos * freq;
-        s.cosv[i] = libm::cosf(val);
-        s.sinv[i] = libm::sinf(val);
+// The fused integer k-quant GEMV applies when every matrix is Q4_K in the
+// integer regime or Q6_K (always integer, linear_dispatch arm Q6_K), and the
+// shapes fit the rows kernel.
+bool fused_args(const vtqrt_model* m, int regime, int epi, std::initializer_list<const Lin*> ws,
+                std::initializer_list<int> rows, size_t norm_off, int in_feat, vtq::RowsArgs* a, int* type) {
+    *a = vtq::RowsArgs{{nullptr, nullptr, nullptr}, {0, 0, 0}, f32_at(m, norm_off), m->eps};
+    *type = -1;
+    int i = 0;
+    for (const Lin* w : ws) {
+        if ((*type >= 0 && w->type != *type) || !(w->type == 14 || (w->type == 12 && regime == 0))) return false;
+        *type = w->type;
+        a->w[i++] = m->dblob + w->offset;
     }
-    const float sq = libm::sqrtf((float)head);
-    for (int l = 0; l < m->layers; l++) {
+    i = 0;
+    for (int r : rows) a->rows[i++] = r;
+    for (int k = 0; k < 3; k++)
+        if (!a->w[k]) a->w[k] = a->w[0];
+    return vtq::kquant_fused_supported(*type, in_feat, epi, *a);
+}
+
+int launch_fused(vtqrt_model* m, int type, int epi, const float* x, const vtq::RowsArgs& a, int in_feat, float* y) {
+    return hip_check(m, vtq::launch_kquant_fused(type, epi, x, a, y, in_feat, m->num_cus, m->stream), "fused linear");
+}
+
+// rms_norm(x, w) into xb for linears that do not normalise in their own prologue
+int norm_to_xb(vtqrt_model* m, size_t w_off) {
+    return hip_check(m, vtq::decode::rms_norm(m->x, f32_at(m, w_off), m->dim, m->eps, m->xb, m->stream), "rms_norm");
+}
+
+vtq::decode::RopeArgs rope_args(vtqrt_model* m) {
+    return vtq::decode::RopeArgs{m->rope, m->dim / m->heads, m->theta};
+}
+
+vtq::decode::EmbedArgs embed_args(vtqrt_model* m) {
+    return vtq::decode::EmbedArgs{m->tok.type, m->dblob + m->tok.offset, table_rows(m),
+                                  vtq::decode::embed_row_bytes(m->tok.type, m->dim), m->dim, m->x, rope_args(m)};
+}
+
+// One decode step at position *m->pos (forward_quantized::step), enqueued
+// on m->stream.  x holds the step's embedding row on entry (the previous
+// step's argmax kernel, or the run's first embedding, wrote it).
+int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* hist) {
+    namespace dec = vtq::decode;
+    const int dim = m->dim, head = dim / m->heads, kv_dim = m->kv_heads * head, hidden = m->hidden;
+    int rc = VTQ_OK, type;
+    vtq::RowsArgs fa;
+    for (int l = 0; !rc && l < m->layers; l++) {
         const Layer& Ly = m->L[l];
-        rms_norm(s.x.data(), Ly.rms_att, dim, m->eps, s.xb.data());
-        rc = linears(m, regime, s.xb.data(), dim,
-                     {{&Ly.wq, m->heads * head, s.q.data()}, {&Ly.wk, kv_dim, s.k.data()}, {&Ly.wv, kv_dim, s.v.data()}});
-        if (rc) return rc;
-        if (Ly.bq) for (int i = 0; i < dim; i++) s.q[i] += Ly.bq[i];
-        if (Ly.bk) for (int i = 0; i < kv_dim; i++) s.k[i] += Ly.bk[i];
-        if (Ly.bv) for (int i = 0; i < kv_dim; i++) s.v[i] += Ly.bv[i];
-        const size_t loff = (size_t)l * m->seq * kv_dim;
-        float* kc = s.kc.data() + loff + (size_t)pos * kv_dim;
-        std::memcpy(kc, s.k.data(), (size_t)kv_dim * 4);
-        std::memcpy(s.vc.data() + loff + (size_t)pos * kv_dim, s.v.data(), (size_t)kv_dim * 4);
-        if (m->neox) {
-            const int half = head / 2;
-            for (int h = 0; h < m->heads; h++)
-                for (int j = 0; j < half; j++) {
-                    float* qb = s.q.data() + h * head;
-                    const float a = qb[j], b = qb[j + half];
-                    qb[j] = a * s.cosv[j] - b * s.sinv[j];
-                    qb[j + half] = a * s.sinv[j] + b * s.cosv[j];
-                }
-            for (int h = 0; h < kv_dim / head; h++)
-                for (int j = 0; j < half; j++) {
-                    float* kb = kc + h * head;
-                    const float a = kb[j], b = kb[j + half];
-                    kb[j] = a * s.cosv[j] - b * s.sinv[j];
-                    kb[j + half] = a * s.sinv[j] + b * s.cosv[j];
-                }
+        // q | k | v = W (rms_norm(x, attn_norm))
+        if (fused_args(m, regime, vtq::kEpiStore, {&Ly.wq, &Ly.wk, &Ly.wv}, {dim, kv_dim, kv_dim}, Ly.rms_att, dim, &fa,
+                       &type)) {
+            rc = launch_fused(m, type, vtq::kEpiStore, m->x, fa, dim, m->qkv);
         } else {
-            for (int i = 0; i < dim; i += 2) {
-                const float fcr = s.cosv[i / 2], fci = s.sinv[i / 2];
-                const float q0 = s.q[i], q1 = s.q[i + 1];
-                s.q[i] = q0 * fcr - q1 * fci;
-                s.q[i + 1] = q0 * fci + q1 * fcr;
-                if (i < kv_dim) {
-                    const float k0 = kc[i], k1 = kc[i + 1];
-                    kc[i] = k0 * fcr - k1 * fci;
-                    kc[i + 1] = k0 * fci + k1 * fcr;
-                }
-            }
+            rc = norm_to_xb(m, Ly.rms_att);
+            if (!rc) rc = linear(m, regime, Ly.wq, m->xb, dim, dim, m->qkv);
+            if (!rc) rc = linear(m, regime, Ly.wk, m->xb, dim, kv_dim, m->qkv + dim);
+            if (!rc) rc = linear(m, regime, Ly.wv, m->xb, dim, kv_dim, m->qkv + dim + kv_dim);
         }
-        // attention, one head per pool item
-        m->pool->parallel_for(m->heads, [&](int h) {
-            float* att = s.att.data() + (size_t)h * m->seq;
-            const float* qh = s.q.data() + h * head;
-            for (int t = 0; t <= pos; t++) {
-                const float* kt = s.kc.data() + loff + (size_t)t * kv_dim + (size_t)(h / kv_mul) * head;
-                float score = 0.0f;
-                for (int d = 0; d < head; d++) score += qh[d] * kt[d];
-                score /= sq;
-                att[t] = score;
-            }
-            float mx = -__builtin_inff();
-            for (int t = 0; t <= pos; t++)
-                if (att[t] > mx) mx = att[t];
-            float sum = 0.0f;
-            for (int t = 0; t <= pos; t++) {
-                att[t] = libm::expf(att[t] - mx);
-                sum += att[t];
-            }
-            const float inv = 1.0f / sum;
-            for (int t = 0; t <= pos; t++) att[t] *= inv;
-            float* xo = s.xo.data() + h * head;
-            for (int d = 0; d < head; d++) xo[d] = 0.0f;
-            for (int t = 0; t <= pos; t++) {
-                const float* vt = s.vc.data() + loff + (size_t)t * kv_dim + (size_t)(h / kv_mul) * head;
-                const float a = att[t];
-                for (int d = 0; d < head; d++) xo[d] += a * vt[d];
-            }
-        });
-        rc = linears(m, regime, s.xo.data(), dim, {{&Ly.wo, dim, s.x2.data()}});
-        if (rc) return rc;
-        for (int i = 0; i < dim; i++) s.x[i] = s.x[i] + s.x2[i];
-        rms_norm(s.x.data(), Ly.rms_ffn, dim, m->eps, s.xb.data());
-        rc = linears(m, regime, s.xb.data(), dim, {{&Ly.w1, hidden, s.gate.data()}, {&Ly.w3, hidden, s.up.data()}});
-        if (rc) return rc;
-        for (int i = 0; i < hidden; i++) {
-            const float g = s.gate[i];
-            const float silu = g / (1.0f + libm::expf(-g));
-            s.ffn[i] = silu * s.up[i];
+        if (rc) break;
+        dec::AttnArgs a;
+        a.qkv = m->qkv;
+        a.bq = f32_at(m, Ly.bq);
+        a.bk = f32_at(m, Ly.bk);
+        a.bv = f32_at(m, Ly.bv);
+        a.kc = m->kc + (size_t)l * m->seq * kv_dim;
+        a.vc = m->vc + (size_t)l * m->seq * kv_dim;
+        a.cs = m->rope;
+        a.out = m->att;
+        a.pos = m->pos;
+        a.heads = m->heads;
+        a.kv_heads = m->kv_heads;
+        a.head_dim = head;
+        a.seq = m->seq;
+        a.theta = m->theta;
+        a.neox = m->neox ? 1 : 0;
+        if ((rc = hip_check(m, dec::attention(a, m->stream), "attention"))) break;
+        // x = x + Wo att
+        if (fused_args(m, regime, vtq::kEpiAccumulate, {&Ly.wo}, {dim}, 0, dim, &fa, &type)) {
+            rc = launch_fused(m, type, vtq::kEpiAccumulate, m->att, fa, dim, m->x);
+        } else {
+            rc = linear(m, regime, Ly.wo, m->att, dim, dim, m->tmp);
+            if (!rc) rc = hip_check(m, dec::add_inplace(m->x, m->tmp, dim, m->stream), "residual");
         }
-        rc = linears(m, regime, s.ffn.data(), hidden, {{&Ly.w2, dim, s.x2.data()}});
-        if (rc) return rc;
-        for (int i = 0; i < dim; i++) s.x[i] = s.x[i] + s.x2[i];
+        if (rc) break;
+        // ffn = silu(W1 h) * (W3 h), h = rms_norm(x, ffn_norm)
+        if (fused_args(m, regime, vtq::kEpiSwiGLU, {&Ly.w1, &Ly.w3}, {hidden, hidden}, Ly.rms_ffn, dim, &fa, &type)) {
+            rc = launch_fused(m, type, vtq::kEpiSwiGLU, m->x, fa, dim, m->ffn);
+        } else {
+            rc = norm_to_xb(m, Ly.rms_ffn);
+            if (!rc) rc = linear(m, regime, Ly.w1, m->xb, dim, hidden, m->gate);
+            if (!rc) rc = linear(m, regime, Ly.w3, m->xb, dim, hidden, m->up);
+            if (!rc) rc = hip_check(m, dec::swiglu(m->gate, m->up, m->ffn, hidden, m->stream), "swiglu");
+        }
+        if (rc) break;
+        // x = x + W2 ffn
+        if (fused_args(m, regime, vtq::kEpiAccumulate, {&Ly.w2}, {dim}, 0, hidden, &fa, &type)) {
+            rc = launch_fused(m, type, vtq::kEpiAccumulate, m->ffn, fa, hidden, m->x);
+        } else {
+            rc = linear(m, regime, Ly.w2, m->ffn, hidden, dim, m->tmp);
+            if (!rc) rc = hip_check(m, dec::add_inplace(m->x, m->tmp, dim, m->stream), "residual");
+        }
     }
-    rms_norm(s.x.data(), m->rms_final, dim, m->eps, s.xb.data());
-    return linears(m, regime, s.xb.data(), dim, {{m->shared ? &m->tok : &m->wcls, m->vocab, s.logits.data()}});
+    if (rc) return rc;
+    // logits = W_out (rms_norm(x, output_norm))
+    const Lin& head_w = m->shared ? m->tok : m->wcls;
+    if (fused_args(m, regime, vtq::kEpiStore, {&head_w}, {m->vocab}, m->rms_final, dim, &fa, &type)) {
+        rc = launch_fused(m, type, vtq::kEpiStore, m->x, fa, dim, m->logits);
+    } else {
+        rc = norm_to_xb(m, m->rms_final);
+        if (!rc) rc = linear(m, regime, head_w, m->xb, dim, m->vocab, m->logits);
+    }
+    if (rc) return rc;
+    return hip_check(m, dec::argmax_advance(m->logits, m->vocab, m->tokens, m->pos, prompt_len, total, hist,
+                                            embed_args(m), m->stream),
+                     "argmax");
 }
 
 const Meta* meta(const std::map<std::string, Meta>& kv, const std::string& k) {
@@ -660,11 +471,10 @@ int vtqrt_dims(const vtqrt_model* m, int dims[7]) {
 void vtqrt_free(vtqrt_model* m) {
     if (!m) return;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
-    if (m->dblob) (void)hipFree(m->dblob);
-    if (m->dx) (void)hipFree(m->dx);
-    if (m->dy) (void)hipFree(m->dy);
-    if (m->hx) (void)hipHostFree(m->hx);
-    if (m->hy) (void)hipHostFree(m->hy);
+    for (void* p : {(void*)m->dblob, (void*)m->x, (void*)m->xb, (void*)m->qkv, (void*)m->att, (void*)m->ffn,
+                    (void*)m->gate, (void*)m->up, (void*)m->tmp, (void*)m->logits, (void*)m->kc, (void*)m->vc,
+                    (void*)m->hist, (void*)m->tokens, (void*)m->pos, (void*)m->rope})
+        if (p) (void)hipFree(p);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     if (m->ctx) vtq_destroy(m->ctx);
     delete m;
@@ -771,11 +581,11 @@ int vtqrt_load(int device, const uint8_t* gguf, size_t len, vtqrt_model** out) {
         o->nbytes = it->second.nbytes;
         return true;
     };
-    auto f32 = [&](const std::string& n, size_t want, bool required, const float** o) {
+    auto f32 = [&](const std::string& n, size_t want, bool required, size_t* o) {
         auto it = ts.find(n);
         if (it == ts.end()) return !required;
-        if (it->second.type != 0 || it->second.nbytes != want * 4) return false;
-        *o = reinterpret_cast<const float*>(m->blob.data() + it->second.offset);
+        if (it->second.type != 0 || it->second.nbytes != want * 4 || it->second.offset % 4) return false;
+        *o = it->second.offset;
         return true;
     };
     const int head = m->dim / m->heads, kv_dim = m->kv_heads * head;
@@ -808,17 +618,24 @@ int vtqrt_load(int device, const uint8_t* gguf, size_t len, vtqrt_model** out) {
         *out = m;
         return rc;
     }
-    const size_t act = 3 * (size_t)std::max({m->dim, m->hidden, m->vocab}) + 256;  // up to 3 outputs per upload
-    if ((rc = hip_check(m, hipMalloc(&m->dx, act * 4), "hipMalloc(x)")) ||
-        (rc = hip_check(m, hipMalloc(&m->dy, act * 4), "hipMalloc(y)")) ||
-        (rc = hip_check(m, hipHostMalloc(&m->hx, act * 4, hipHostMallocDefault), "hipHostMalloc(x)")) ||
-        (rc = hip_check(m, hipHostMalloc(&m->hy, act * 4, hipHostMallocDefault), "hipHostMalloc(y)"))) {
+    m->device = device;
+    if ((rc = hip_check(m, hipDeviceGetAttribute(&m->num_cus, hipDeviceAttributeMultiprocessorCount, device),
+                        "hipDeviceGetAttribute"))) {
         *out = m;
         return rc;
     }
-    const unsigned hw = std::thread::hardware_concurrency();
-    const int threads = (int)std::min<unsigned>(hw ? hw : 1, 16);
-    m->pool.reset(new Pool(std::max(0, threads - 1)));
+    const size_t kv_elems = (size_t)m->layers * m->seq * kv_dim;
+    auto dalloc = [&](auto** p, size_t n) {
+        return hip_check(m, hipMalloc(reinterpret_cast<void**>(p), std::max<size_t>(n, 1) * 4), "hipMalloc(state)");
+    };
+    if ((rc = dalloc(&m->x, m->dim)) || (rc = dalloc(&m->xb, m->dim)) || (rc = dalloc(&m->qkv, m->dim + 2 * kv_dim)) ||
+        (rc = dalloc(&m->att, m->dim)) || (rc = dalloc(&m->ffn, m->hidden)) || (rc = dalloc(&m->gate, m->hidden)) ||
+        (rc = dalloc(&m->up, m->hidden)) || (rc = dalloc(&m->tmp, m->dim)) || (rc = dalloc(&m->logits, m->vocab)) ||
+        (rc = dalloc(&m->kc, kv_elems)) || (rc = dalloc(&m->vc, kv_elems)) || (rc = dalloc(&m->tokens, m->seq + 1)) ||
+        (rc = dalloc(&m->pos, 1)) || (rc = dalloc(&m->rope, head))) {
+        *out = m;
+        return rc;
+    }
     *out = m;
     return VTQ_OK;
 }
@@ -833,43 +650,77 @@ int vtqrt_run(vtqrt_model* m, int regime, const char* model_id, const uint8_t we
     if (prompt_len <= 0) return fail(m, VTQ_E_INTERNAL, "prompt_tokens must not be empty");
     const int total = prompt_len + n_new;
     if (total > m->seq) return fail(m, VTQ_E_INTERNAL, "prompt + n_new_tokens exceeds seq_len");
-    const int head = m->dim / m->heads, kv_dim = m->kv_heads * head;
-    State s;
-    const size_t kv = (size_t)m->layers * m->seq * kv_dim;
-    s.kc.assign(kv, 0.0f);
-    s.vc.assign(kv, 0.0f);
-    s.x.resize(m->dim);
-    s.xb.resize(m->dim);
-    s.q.resize(m->dim);
-    s.k.resize(kv_dim);
-    s.v.resize(kv_dim);
-    s.xo.resize(m->dim);
-    s.x2.resize(m->dim);
-    s.gate.resize(m->hidden);
-    s.up.resize(m->hidden);
-    s.ffn.resize(m->hidden);
-    s.logits.resize(m->vocab);
-    s.cosv.resize(m->dim);
-    s.sinv.resize(m->dim);
-    s.att.resize((size_t)m->heads * m->seq);
-    std::vector<uint32_t> gen;
-    uint32_t cur = prompt[0];
-    for (int pos = 0; pos < total; pos++) {
-        if (cur >= (uint32_t)m->vocab) return fail(m, VTQ_E_INTERNAL, "embedding_row: row past end of table");
-        int rc = step(m, s, regime, cur, pos);
-        if (rc) return rc;
-        if (logits) std::memcpy(logits + (size_t)pos * m->vocab, s.logits.data(), (size_t)m->vocab * 4);
-        uint32_t best = 0;
-        float bv = s.logits[0];
-        for (int i = 1; i < m->vocab; i++)
-            if (s.logits[i] > bv) {
-                bv = s.logits[i];
-                best = (uint32_t)i;
-            }
-        const uint32_t next = pos + 1 < prompt_len ? prompt[pos + 1] : best;
-        if (pos >= prompt_len) gen.push_back(next);
-        cur = next;
+    if (!vtq::decode::embed_row_bytes(m->tok.type, m->dim))
+        return fail(m, VTQ_E_NOT_IMPLEMENTED, "embedding_row: non-Q4_0 / Q4_K / Q6_K / Q8_0 / F32 embedding dtype");
+    if ((m->dim / m->heads) % 2)
+        return fail(m, VTQ_E_NOT_IMPLEMENTED, "RoPE: odd head dimension");
+    const uint32_t rows = table_rows(m);
+    for (int i = 0; i < prompt_len; i++)
+        if (prompt[i] >= rows) return fail(m, VTQ_E_INTERNAL, "embedding_row: row past end of table");
+    int rc = hip_check(m, hipSetDevice(m->device), "hipSetDevice");
+    if (rc) return rc;
+    if (logits && m->hist_cap < (size_t)total * m->vocab) {
+        if (m->hist) (void)hipFree(m->hist);
+        m->hist = nullptr;
+        m->hist_cap = 0;
+        if ((rc = hip_check(m, hipMalloc(&m->hist, (size_t)total * m->vocab * 4), "hipMalloc(logits)"))) return rc;
+        m->hist_cap = (size_t)total * m->vocab;
     }
+    float* hist = logits ? m->hist : nullptr;
+    // tokens[0 .. prompt_len) = prompt; step p reads tokens[p] and its argmax
+    // writes tokens[p + 1] once p + 1 >= prompt_len
+    const int zero = 0;
+    if ((rc = hip_check(m, hipMemcpyAsync(m->tokens, prompt, (size_t)prompt_len * 4, hipMemcpyHostToDevice, m->stream),
+                        "hipMemcpyAsync(prompt)")) ||
+        (rc = hip_check(m, hipMemcpyAsync(m->pos, &zero, 4, hipMemcpyHostToDevice, m->stream), "hipMemcpyAsync(pos)")) ||
+        (rc = hip_check(m, hipStreamSynchronize(m->stream), "hipStreamSynchronize")))
+        return rc;
+    // capture one step and replay it per position; launch eagerly when the
+    // graph cannot be built (or VTQRT_EAGER is set)
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    const char* eager_env = std::getenv("VTQRT_EAGER");
+    if (!(eager_env && *eager_env && *eager_env != '0') &&
+        hipStreamBeginCapture(m->stream, hipStreamCaptureModeRelaxed) == hipSuccess) {
+        const int crc = enqueue_step(m, regime, prompt_len, total, hist);
+        const hipError_t ce = hipStreamEndCapture(m->stream, &graph);
+        if (crc || ce != hipSuccess || !graph || hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+            if (exec) (void)hipGraphExecDestroy(exec);
+            exec = nullptr;
+            (void)hipGetLastError();
+            m->err.clear();
+        }
+        if (graph) (void)hipGraphDestroy(graph);
+    }
+    rc = hip_check(m, vtq::decode::embed(m->tok.type, m->dblob + m->tok.offset, table_rows(m), m->tokens, m->pos, m->dim,
+                                         m->x, rope_args(m), m->stream),
+                   "embedding_row");
+    for (int pos = 0; pos < total && !rc; pos++)
+        rc = exec ? hip_check(m, hipGraphLaunch(exec, m->stream), "hipGraphLaunch")
+                  : enqueue_step(m, regime, prompt_len, total, hist);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (rc) {
+        (void)hipStreamSynchronize(m->stream);
+        return rc;
+    }
+    // tokens[prompt_len .. total]: fed[i] was consumed by step prompt_len + i
+    // (i < n_new); the generated tokens are fed[1 ..] (run_quantized pushes
+    // the pick of steps prompt_len .. total-1)
+    std::vector<uint32_t> fed((size_t)n_new + 1);
+    if (n_new > 0 &&
+        (rc = hip_check(m, hipMemcpyAsync(fed.data(), m->tokens + prompt_len, (size_t)(n_new + 1) * 4,
+                                          hipMemcpyDeviceToHost, m->stream),
+                        "hipMemcpyAsync(tokens)")))
+        return rc;
+    if (logits && (rc = hip_check(m, hipMemcpyAsync(logits, hist, (size_t)total * m->vocab * 4, hipMemcpyDeviceToHost,
+                                                    m->stream),
+                                  "hipMemcpyAsync(logits)")))
+        return rc;
+    if ((rc = hip_check(m, hipStreamSynchronize(m->stream), "hipStreamSynchronize"))) return rc;
+    // a picked token that a step consumed must name a table row
+    for (int i = 0; i < n_new; i++)
+        if (fed[i] >= rows) return fail(m, VTQ_E_INTERNAL, "embedding_row: row past end of table");
+    std::vector<uint32_t> gen(fed.begin() + 1, fed.end());
     std::memcpy(tokens, gen.data(), gen.size() * 4);
     // the receipt: inputs then outputs, length-prefixed (inference.rs:300-333)
     char arch[256];
