@@ -79,6 +79,12 @@ def lib() -> ctypes.CDLL:
         getattr(L, name).restype = f
     L.vtqo_powf.argtypes = [f, f]
     L.vtqo_powf.restype = f
+    L.vtqo_rms_norm.argtypes = [vp, vp, i, f, vp]
+    L.vtqo_rms_norm.restype = None
+    L.vtqo_softmax.argtypes = [vp, i]
+    L.vtqo_softmax.restype = None
+    L.vtqo_argmax.argtypes = [vp, i]
+    L.vtqo_argmax.restype = ctypes.c_uint32
     L.vtqo_blake3_hash.argtypes = [vp, sz, vp]
     L.vtqo_blake3_hash.restype = None
     L.vtqo_transcendental_hash.argtypes = [vp]
@@ -353,6 +359,28 @@ def sinf(v: float) -> np.float32:
 
 def cosf(v: float) -> np.float32:
     return np.float32(lib().vtqo_cosf(v))
+
+
+def rms_norm(x, w, eps) -> np.ndarray:
+    """rms_norm_slice (src/ops/rms_norm.rs:60-110) of one row."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().vtqo_rms_norm(_ptr(x), _ptr(w), x.size, eps, _ptr(out))
+    return out
+
+
+def softmax(x) -> np.ndarray:
+    """softmax_inplace (src/model/forward_quantized.rs:925-941), on a copy."""
+    v = np.array(x, dtype=np.float32)
+    lib().vtqo_softmax(_ptr(v), v.size)
+    return v
+
+
+def argmax(v) -> int:
+    """argmax_last_dim (src/ops/argmax.rs:21-68) of one row."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    return int(lib().vtqo_argmax(_ptr(v), v.size))
 
 
 def blake3(data) -> str:

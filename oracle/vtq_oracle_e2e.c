@@ -10,6 +10,14 @@
  * inference::run_quantized (src/model/inference.rs:274-345) with its
  * receipt (src/cert/builder.rs:458-471).  Linears go through
  * vtqo_linear_dispatch (forward_quantized.rs:663-785).
+ *
+ * Pins: the libm and BLAKE3 restatements and the v2 digest are pinned by the
+ * reference's own constants (tests/test_oracle_e2e.py); rms_norm, softmax
+ * and argmax by the reference's known answers (src/ops/rms_norm.rs:117-160,
+ * src/ops/argmax.rs:74-125) and closed forms.  Parity unpinned: the
+ * composition of the forward step and run_quantized's token loop -- the
+ * reference's model tests need GGUF files that are not in the repository,
+ * and no reference-produced logits exist for any model here.
  */
 #include "vtq_oracle_e2e.h"
 #include "vtq_oracle.h"
@@ -381,7 +389,7 @@ static int linear(run_t* r, const qt_t* w, const float* x, int in_f, int out_f, 
 }
 
 /* rms_norm_slice (src/ops/rms_norm.rs:60-110) */
-static void rms_norm(const float* x, const float* w, int n, float eps, float* out) {
+void vtqo_rms_norm(const float* x, const float* w, int n, float eps, float* out) {
     float sumsq = 0.0f;
     for (int i = 0; i < n; i++) sumsq += x[i] * x[i];
     const float mean = sumsq / (float)n;
@@ -390,7 +398,7 @@ static void rms_norm(const float* x, const float* w, int n, float eps, float* ou
 }
 
 /* softmax_inplace (src/model/forward_quantized.rs:925-941) */
-static void softmax(float* x, int n) {
+void vtqo_softmax(float* x, int n) {
     float max = -INFINITY;
     for (int i = 0; i < n; i++)
         if (x[i] > max) max = x[i];
@@ -438,7 +446,7 @@ static int step(run_t* r, uint32_t token, int pos) {
     if (embedding_row(r, &m->tok_embd, (int)token, dim, r->x)) return 1;
     for (int l = 0; l < m->n_layers; l++) {
         const layer_t* L = &m->layers[l];
-        rms_norm(r->x, L->rms_att, dim, m->rms_eps, r->xb);
+        vtqo_rms_norm(r->x, L->rms_att, dim, m->rms_eps, r->xb);
         if (linear(r, &L->wq, r->xb, dim, m->n_heads * head, r->q)) return 1;
         if (L->bq) for (int i = 0; i < dim; i++) r->q[i] += L->bq[i];
         if (linear(r, &L->wk, r->xb, dim, kv_dim, r->k)) return 1;
@@ -496,7 +504,7 @@ static int step(run_t* r, uint32_t token, int pos) {
                 score /= sq;
                 r->att[t] = score;
             }
-            softmax(r->att, pos + 1);
+            vtqo_softmax(r->att, pos + 1);
             float* xo = r->xb_out + h * head;
             for (int t = 0; t <= pos; t++) {
                 const float* vt = r->value_cache + loff + (size_t)t * kv_dim + (size_t)(h / kv_mul) * head;
@@ -506,7 +514,7 @@ static int step(run_t* r, uint32_t token, int pos) {
         }
         if (linear(r, &L->wo, r->xb_out, dim, dim, r->xb2)) return 1;
         for (int i = 0; i < dim; i++) r->x[i] = r->x[i] + r->xb2[i];
-        rms_norm(r->x, L->rms_ffn, dim, m->rms_eps, r->xb);
+        vtqo_rms_norm(r->x, L->rms_ffn, dim, m->rms_eps, r->xb);
         if (linear(r, &L->w1, r->xb, dim, hidden, r->gate)) return 1;
         if (linear(r, &L->w3, r->xb, dim, hidden, r->up)) return 1;
         for (int i = 0; i < hidden; i++) {
@@ -517,12 +525,12 @@ static int step(run_t* r, uint32_t token, int pos) {
         if (linear(r, &L->w2, r->ffn, hidden, dim, r->xb2)) return 1;
         for (int i = 0; i < dim; i++) r->x[i] = r->x[i] + r->xb2[i];
     }
-    rms_norm(r->x, m->rms_final, dim, m->rms_eps, r->xb);
+    vtqo_rms_norm(r->x, m->rms_final, dim, m->rms_eps, r->xb);
     return linear(r, m->shared ? &m->tok_embd : &m->wcls, r->xb, dim, m->vocab, r->logits);
 }
 
 /* argmax_last_dim (src/ops/argmax.rs:21-68): first maximum, strict > */
-static uint32_t argmax(const float* v, int n) {
+uint32_t vtqo_argmax(const float* v, int n) {
     int best = 0;
     float bv = v[0];
     for (int i = 1; i < n; i++)
@@ -583,7 +591,7 @@ int vtqo_run_quantized(const vtqo_model* m, int regime, const char* model_id, co
     for (int pos = 0; pos < total; pos++) {
         if ((rc = step(&r, cur, pos))) break;
         if (logits) memcpy(logits + (size_t)pos * m->vocab, r.logits, (size_t)m->vocab * 4);
-        const uint32_t picked = argmax(r.logits, m->vocab);
+        const uint32_t picked = vtqo_argmax(r.logits, m->vocab);
         const uint32_t next = pos + 1 < prompt_len ? prompt[pos + 1] : picked;
         if (pos >= prompt_len) tokens[n_gen++] = next;
         cur = next;

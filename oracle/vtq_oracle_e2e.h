@@ -77,6 +77,11 @@ int vtqo_run_quantized(const vtqo_model *m, int regime, const char *model_id, co
                        const uint32_t *prompt, int prompt_len, int n_new, int threads, float *logits,
                        uint32_t *tokens, uint8_t digest[32], const char **msg);
 
+/* forward-step helpers, exported for their known-answer tests */
+void vtqo_rms_norm(const float* x, const float* w, int n, float eps, float* out);
+void vtqo_softmax(float* x, int n);
+uint32_t vtqo_argmax(const float* v, int n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -6,6 +6,9 @@
 * BLAKE3: the published empty-input vector, and the multi-chunk stream of the
   transcendental sweep (13.7 MB) through the pin above.
 * receipt: the reference's v2 digest pin (src/cert/builder.rs:719-741).
+* forward-step helpers: the reference's known answers for rms_norm
+  (src/ops/rms_norm.rs:117-160) and argmax (src/ops/argmax.rs:74-125), and
+  closed forms of softmax.
 * GGUF: the synthetic model parses to the configured shape.
 """
 import numpy as np
@@ -84,3 +87,38 @@ def test_run_quantized_errors():
         m.run(prompt, 64, b"\0" * 32)
     with pytest.raises(oracle.OracleError, match="bad magic"):
         oracle.Model(np.frombuffer(b"GGML" + b"\0" * 60, dtype=np.uint8))
+
+
+def test_rms_norm_reference_known_answers():
+    # rms_norm_identity_scale, rms_norm_weighted: exact; rms_norm_known: the
+    # reference's 1e-4 tolerance, and the bits of x * (1/sqrt(12.5)) * 1
+    assert np.array_equal(oracle.rms_norm(np.ones(4), np.ones(4), 0.0), np.ones(4, dtype=np.float32))
+    assert np.array_equal(oracle.rms_norm([1.0, 1.0], [2.0, 3.0], 0.0), np.array([2.0, 3.0], dtype=np.float32))
+    y = oracle.rms_norm([3.0, 4.0], [1.0, 1.0], 0.0)
+    assert abs(y[0] - 0.8485281) < 1e-4 and abs(y[1] - 1.1313708) < 1e-4
+    scale = np.float32(1.0) / np.sqrt(np.float32(12.5))  # sum 25 and mean 12.5 are exact
+    assert y.tobytes() == (np.array([3.0, 4.0], dtype=np.float32) * scale).tobytes()
+    # the sum of squares is serial: 1 + 2^-24 + 2^-24 rounds each add back to 1
+    x = np.array([1.0, 2.0 ** -12, 2.0 ** -12], dtype=np.float32)
+    serial = oracle.rms_norm(x, np.ones(3), 0.0)
+    scale = np.float32(1.0) / np.sqrt(np.float32(1.0) / np.float32(3.0))
+    assert serial.tobytes() == (x * scale).tobytes()
+
+
+def test_argmax_reference_known_answers():
+    assert oracle.argmax([0.1, 0.5, 0.3, 0.8, 0.2]) == 3          # argmax_simple
+    assert oracle.argmax([0.1, 0.5, 0.3, 0.5, 0.2]) == 1          # argmax_tie_picks_first
+    assert oracle.argmax([0.1, 0.5, 0.3]) == 1 and oracle.argmax([0.9, 0.2, 0.4]) == 0  # argmax_per_row
+    nan = float("nan")
+    assert oracle.argmax([nan, 5.0, 7.0]) == 0                      # nothing is > NaN at index 0
+    assert oracle.argmax([1.0, nan, 7.0, 7.0]) == 2                 # later NaNs never win
+    assert oracle.argmax([-0.0, 0.0]) == 0                          # +0 > -0 is false
+
+
+def test_softmax_closed_forms():
+    for n in (1, 2, 4, 64, 256):
+        assert np.array_equal(oracle.softmax(np.full(n, 3.5)), np.full(n, 1.0 / n, dtype=np.float32))
+    y = oracle.softmax([0.0, float(np.log(3.0))])
+    assert abs(float(y.sum()) - 1.0) < 1e-6 and y[1] > y[0]
+    # the max is subtracted first: huge equal inputs do not overflow
+    assert np.array_equal(oracle.softmax([1e30, 1e30]), np.array([0.5, 0.5], dtype=np.float32))
