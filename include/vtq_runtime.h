@@ -50,6 +50,34 @@ int vtqrt_run(vtqrt_model *m, int regime, const char *model_id, const uint8_t we
               const uint32_t *prompt, int prompt_len, int n_new, float *logits, uint32_t *tokens,
               uint8_t digest[32]);
 
+/* run_quantized with a PerOpRecorder and/or a PerActivationRecorder attached
+ * to every step (src/model/forward_quantized.rs:64-132, :260-284,
+ * step_with_recorders :329-655): per op, BLAKE3 of its f32 input and output
+ * and of its weights (hash_f32_slice for norms); per checkpoint (post_embed,
+ * post_attn, post_ffn, pre_lm_head, post_lm_head) BLAKE3 of the residual
+ * stream.  The records enter the v2 digest in declaration order
+ * (src/cert/builder.rs:251-305, :489-560).  op_name is "rms_norm" or
+ * "linear_q4_0" (the reference's name for every linear); layer is
+ * 0xFFFFFFFF for the model-level ops.  ops / acts (optional) receive up to
+ * *_cap records, *n_ops / *n_acts the counts (9*layers + 2 and
+ * 2*layers + 3 per step). */
+#define VTQRT_RECORD_OPS 1
+#define VTQRT_RECORD_ACTIVATIONS 2
+typedef struct {
+    uint32_t op_index, layer;
+    char op_name[16];
+    uint8_t input_hash[32], params_hash[32], output_hash[32];
+} vtqrt_op_record;
+typedef struct {
+    uint32_t act_index, token_index, layer;
+    char checkpoint[16];
+    uint8_t tensor_hash[32];
+} vtqrt_act_record;
+int vtqrt_run_recorded(vtqrt_model *m, int regime, const char *model_id, const uint8_t weights_hash[32],
+                       const uint32_t *prompt, int prompt_len, int n_new, int flags, uint32_t *tokens,
+                       vtqrt_op_record *ops, size_t ops_cap, vtqrt_act_record *acts, size_t acts_cap,
+                       size_t *n_ops, size_t *n_acts, uint8_t digest[32]);
+
 /* BLAKE3-256 (crate blake3 = "1" as the reference uses it). */
 void vtqrt_blake3(const void *data, size_t len, uint8_t out[32]);
 

@@ -79,6 +79,9 @@ def lib() -> ctypes.CDLL:
         getattr(L, name).restype = f
     L.vtqo_powf.argtypes = [f, f]
     L.vtqo_powf.restype = f
+    L.vtqo_run_quantized_recorded.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, i, i, vp, vp, sz, vp, sz,
+                                              ctypes.POINTER(sz), ctypes.POINTER(sz), vp, msgp]
+    L.vtqo_run_quantized_recorded.restype = i
     L.vtqo_rms_norm.argtypes = [vp, vp, i, f, vp]
     L.vtqo_rms_norm.restype = None
     L.vtqo_softmax.argtypes = [vp, i]
@@ -414,6 +417,31 @@ def digest_v2(inputs, outputs) -> str:
     return bytes(out).hex()
 
 
+RECORD_OPS = 1
+RECORD_ACTIVATIONS = 2
+NO_LAYER = 0xFFFFFFFF
+
+
+class OpRecord(ctypes.Structure):
+    """OpRecord (src/cert/builder.rs): op_index, layer, op_name, input/params/output hashes."""
+    _fields_ = [("op_index", ctypes.c_uint32), ("layer", ctypes.c_uint32), ("op_name", ctypes.c_char * 16),
+                ("input_hash", ctypes.c_uint8 * 32), ("params_hash", ctypes.c_uint8 * 32),
+                ("output_hash", ctypes.c_uint8 * 32)]
+
+    def key(self):
+        return (self.op_index, self.layer, self.op_name, bytes(self.input_hash), bytes(self.params_hash),
+                bytes(self.output_hash))
+
+
+class ActRecord(ctypes.Structure):
+    """ActivationRecord (src/cert/builder.rs): act_index, token_index, layer, checkpoint, tensor hash."""
+    _fields_ = [("act_index", ctypes.c_uint32), ("token_index", ctypes.c_uint32), ("layer", ctypes.c_uint32),
+                ("checkpoint", ctypes.c_char * 16), ("tensor_hash", ctypes.c_uint8 * 32)]
+
+    def key(self):
+        return (self.act_index, self.token_index, self.layer, self.checkpoint, bytes(self.tensor_hash))
+
+
 class Model:
     """GGUF model for inference::run_quantized (the blob must stay alive)."""
 
@@ -441,6 +469,26 @@ class Model:
         if logits is not None:
             logits = logits.reshape(prompt.size + n_new, self.vocab)
         return tokens[:n_new], bytes(digest).hex(), logits
+
+    def run_recorded(self, prompt, n_new, weights_hash: bytes, flags=RECORD_OPS | RECORD_ACTIVATIONS, regime=0,
+                     model_id="vitni-receipt", threads=1):
+        """run_quantized with per-op / activation recorders on every step:
+        (tokens, digest hex, [OpRecord], [ActRecord])."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        wh = np.frombuffer(bytes(weights_hash), dtype=np.uint8).copy()
+        tokens = np.zeros(max(1, n_new), dtype=np.uint32)
+        steps = prompt.size + n_new
+        ops = (OpRecord * max(1, steps * (9 * self.layers + 2)))()
+        acts = (ActRecord * max(1, steps * (2 * self.layers + 3)))()
+        n_ops, n_acts = ctypes.c_size_t(), ctypes.c_size_t()
+        digest = (ctypes.c_uint8 * 32)()
+        msg = ctypes.c_char_p()
+        rc = lib().vtqo_run_quantized_recorded(self.handle, regime, model_id.encode(), _ptr(wh), _ptr(prompt),
+                                               prompt.size, n_new, threads, flags, _ptr(tokens), ops, len(ops),
+                                               acts, len(acts), ctypes.byref(n_ops), ctypes.byref(n_acts), digest,
+                                               ctypes.byref(msg))
+        _check(rc, msg)
+        return tokens[:n_new], bytes(digest).hex(), list(ops[:n_ops.value]), list(acts[:n_acts.value])
 
     def __del__(self):
         if getattr(self, "handle", None):

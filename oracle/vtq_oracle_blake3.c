@@ -191,9 +191,32 @@ static void field(vtqo_blake3* h, const char* name, const uint8_t* data, size_t 
     vtqo_blake3_update(h, data, len);
 }
 
-void vtqo_digest_v2(int n_in, const char* const* in_names, const uint8_t* const* in_data, const size_t* in_lens,
-                    int n_out, const char* const* out_names, const uint8_t* const* out_data,
-                    const size_t* out_lens, uint8_t out[32]) {
+/* write_op / write_activation (src/cert/builder.rs:525-560) */
+static void write_op(vtqo_blake3* h, const vtqo_op_record* op) {
+    const size_t nl = strlen(op->op_name);
+    leb128(h, op->op_index);
+    leb128(h, nl);
+    vtqo_blake3_update(h, op->op_name, nl);
+    leb128(h, op->layer);
+    vtqo_blake3_update(h, op->input_hash, 32);
+    vtqo_blake3_update(h, op->params_hash, 32);
+    vtqo_blake3_update(h, op->output_hash, 32);
+}
+
+static void write_activation(vtqo_blake3* h, const vtqo_act_record* a) {
+    const size_t nl = strlen(a->checkpoint);
+    leb128(h, a->act_index);
+    leb128(h, a->token_index);
+    leb128(h, a->layer);
+    leb128(h, nl);
+    vtqo_blake3_update(h, a->checkpoint, nl);
+    vtqo_blake3_update(h, a->tensor_hash, 32);
+}
+
+void vtqo_digest_v2_full(int n_in, const char* const* in_names, const uint8_t* const* in_data, const size_t* in_lens,
+                         int n_out, const char* const* out_names, const uint8_t* const* out_data,
+                         const size_t* out_lens, size_t n_ops, const vtqo_op_record* ops, size_t n_acts,
+                         const vtqo_act_record* acts, uint8_t out[32]) {
     static const char kRegime[] = "vitni-regime-1";  /* src/cert/builder.rs:440 */
     vtqo_blake3 h;
     vtqo_blake3_init(&h);
@@ -204,10 +227,19 @@ void vtqo_digest_v2(int n_in, const char* const* in_names, const uint8_t* const*
     for (int i = 0; i < n_in; i++) field(&h, in_names[i], in_data[i], in_lens[i]);
     leb128(&h, (uint64_t)n_out);
     for (int i = 0; i < n_out; i++) field(&h, out_names[i], out_data[i], out_lens[i]);
-    leb128(&h, 0);  /* ops */
-    leb128(&h, 0);  /* activations */
+    leb128(&h, (uint64_t)n_ops);
+    for (size_t i = 0; i < n_ops; i++) write_op(&h, &ops[i]);
+    leb128(&h, (uint64_t)n_acts);
+    for (size_t i = 0; i < n_acts; i++) write_activation(&h, &acts[i]);
     leb128(&h, 0);  /* interventions */
     vtqo_blake3_final(&h, out);
+}
+
+void vtqo_digest_v2(int n_in, const char* const* in_names, const uint8_t* const* in_data, const size_t* in_lens,
+                    int n_out, const char* const* out_names, const uint8_t* const* out_data,
+                    const size_t* out_lens, uint8_t out[32]) {
+    vtqo_digest_v2_full(n_in, in_names, in_data, in_lens, n_out, out_names, out_data, out_lens, 0, NULL, 0, NULL,
+                        out);
 }
 
 /* ---- tests/transcendental_determinism.rs:14-60 ---- */

@@ -375,8 +375,74 @@ void vtqo_model_dims(const vtqo_model* m, int dims[7]) {
 
 /* ---------------------------------------------------------------- step */
 
+/* ---------------------------------------------------------------- receipts */
+
+/* PerOpRecorder / PerActivationRecorder (src/model/forward_quantized.rs:64-132,
+ * :260-284).  params[l][k]: k = 0 rms_att, 1 wq, 2 wk, 3 wv, 4 wo, 5 rms_ffn,
+ * 6 w1, 7 w2, 8 w3 -- BLAKE3 of the weight bytes, hash_f32_slice of norms. */
+#define NO_LAYER 0xFFFFFFFFu
+typedef struct {
+    int flags;
+    uint8_t (*params)[9][32];
+    uint8_t tok[32], rms_final[32], wcls[32];
+    vtqo_op_record* ops;
+    vtqo_act_record* acts;
+    size_t n_ops, cap_ops, n_acts, cap_acts;
+    int oom;
+} rec_t;
+
+/* hash_f32_slice (forward_quantized.rs:275-284): BLAKE3 of the LE bytes */
+static void hash_f32(const float* v, size_t n, uint8_t out[32]) { vtqo_blake3_hash(v, n * 4, out); }
+
+static void rec_op(rec_t* rc, const char* name, uint32_t layer, const uint8_t* params, const float* in, size_t n_in,
+                   const float* out, size_t n_out) {
+    if (!rc || !(rc->flags & VTQO_RECORD_OPS) || rc->oom) return;
+    if (rc->n_ops == rc->cap_ops) {
+        const size_t cap = rc->cap_ops ? 2 * rc->cap_ops : 256;
+        vtqo_op_record* p = (vtqo_op_record*)realloc(rc->ops, cap * sizeof *p);
+        if (!p) {
+            rc->oom = 1;
+            return;
+        }
+        rc->ops = p;
+        rc->cap_ops = cap;
+    }
+    vtqo_op_record* o = &rc->ops[rc->n_ops];
+    memset(o, 0, sizeof *o);
+    o->op_index = (uint32_t)rc->n_ops;
+    o->layer = layer;
+    strncpy(o->op_name, name, sizeof o->op_name - 1);
+    hash_f32(in, n_in, o->input_hash);
+    if (params) memcpy(o->params_hash, params, 32);
+    hash_f32(out, n_out, o->output_hash);
+    rc->n_ops++;
+}
+
+static void rec_act(rec_t* rc, uint32_t token, uint32_t layer, const char* checkpoint, const float* t, size_t n) {
+    if (!rc || !(rc->flags & VTQO_RECORD_ACTIVATIONS) || rc->oom) return;
+    if (rc->n_acts == rc->cap_acts) {
+        const size_t cap = rc->cap_acts ? 2 * rc->cap_acts : 256;
+        vtqo_act_record* p = (vtqo_act_record*)realloc(rc->acts, cap * sizeof *p);
+        if (!p) {
+            rc->oom = 1;
+            return;
+        }
+        rc->acts = p;
+        rc->cap_acts = cap;
+    }
+    vtqo_act_record* a = &rc->acts[rc->n_acts];
+    memset(a, 0, sizeof *a);
+    a->act_index = (uint32_t)rc->n_acts;
+    a->token_index = token;
+    a->layer = layer;
+    strncpy(a->checkpoint, checkpoint, sizeof a->checkpoint - 1);
+    hash_f32(t, n, a->tensor_hash);
+    rc->n_acts++;
+}
+
 typedef struct {
     const vtqo_model* m;
+    rec_t* rec;
     int regime, threads;
     float *key_cache, *value_cache;  /* [layers][seq][kv_dim] */
     float *x, *xb, *q, *k, *v, *att, *xb_out, *xb2, *gate, *up, *ffn, *logits;
@@ -443,15 +509,23 @@ static int step(run_t* r, uint32_t token, int pos) {
     const vtqo_model* m = r->m;
     const int dim = m->dim, head = dim / m->n_heads, kv_dim = m->n_kv_heads * head;
     const int kv_mul = m->n_heads / m->n_kv_heads, hidden = m->hidden;
+    rec_t* rc = r->rec;
+    const uint32_t tk = (uint32_t)pos;
     if (embedding_row(r, &m->tok_embd, (int)token, dim, r->x)) return 1;
+    rec_act(rc, tk, NO_LAYER, "post_embed", r->x, dim);
     for (int l = 0; l < m->n_layers; l++) {
         const layer_t* L = &m->layers[l];
+        const uint8_t(*P)[32] = rc && rc->params ? rc->params[l] : NULL;
         vtqo_rms_norm(r->x, L->rms_att, dim, m->rms_eps, r->xb);
+        rec_op(rc, "rms_norm", (uint32_t)l, P ? P[0] : NULL, r->x, dim, r->xb, dim);
         if (linear(r, &L->wq, r->xb, dim, m->n_heads * head, r->q)) return 1;
+        rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[1] : NULL, r->xb, dim, r->q, (size_t)m->n_heads * head);
         if (L->bq) for (int i = 0; i < dim; i++) r->q[i] += L->bq[i];
         if (linear(r, &L->wk, r->xb, dim, kv_dim, r->k)) return 1;
+        rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[2] : NULL, r->xb, dim, r->k, kv_dim);
         if (L->bk) for (int i = 0; i < kv_dim; i++) r->k[i] += L->bk[i];
         if (linear(r, &L->wv, r->xb, dim, kv_dim, r->v)) return 1;
+        rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[3] : NULL, r->xb, dim, r->v, kv_dim);
         if (L->bv) for (int i = 0; i < kv_dim; i++) r->v[i] += L->bv[i];
         const size_t loff = (size_t)l * m->seq_len * kv_dim;
         float* kc = r->key_cache + loff + (size_t)pos * kv_dim;
@@ -513,20 +587,33 @@ static int step(run_t* r, uint32_t token, int pos) {
             }
         }
         if (linear(r, &L->wo, r->xb_out, dim, dim, r->xb2)) return 1;
+        rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[4] : NULL, r->xb_out, dim, r->xb2, dim);
         for (int i = 0; i < dim; i++) r->x[i] = r->x[i] + r->xb2[i];
+        rec_act(rc, tk, (uint32_t)l, "post_attn", r->x, dim);
         vtqo_rms_norm(r->x, L->rms_ffn, dim, m->rms_eps, r->xb);
+        rec_op(rc, "rms_norm", (uint32_t)l, P ? P[5] : NULL, r->x, dim, r->xb, dim);
         if (linear(r, &L->w1, r->xb, dim, hidden, r->gate)) return 1;
+        rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[6] : NULL, r->xb, dim, r->gate, hidden);
         if (linear(r, &L->w3, r->xb, dim, hidden, r->up)) return 1;
+        rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[8] : NULL, r->xb, dim, r->up, hidden);
         for (int i = 0; i < hidden; i++) {
             const float g = r->gate[i];
             const float silu = g / (1.0f + vtqo_expf(-g));
             r->ffn[i] = silu * r->up[i];
         }
         if (linear(r, &L->w2, r->ffn, hidden, dim, r->xb2)) return 1;
+        rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[7] : NULL, r->ffn, hidden, r->xb2, dim);
         for (int i = 0; i < dim; i++) r->x[i] = r->x[i] + r->xb2[i];
+        rec_act(rc, tk, (uint32_t)l, "post_ffn", r->x, dim);
     }
     vtqo_rms_norm(r->x, m->rms_final, dim, m->rms_eps, r->xb);
-    return linear(r, m->shared ? &m->tok_embd : &m->wcls, r->xb, dim, m->vocab, r->logits);
+    rec_op(rc, "rms_norm", NO_LAYER, rc ? rc->rms_final : NULL, r->x, dim, r->xb, dim);
+    rec_act(rc, tk, NO_LAYER, "pre_lm_head", r->xb, dim);
+    if (linear(r, m->shared ? &m->tok_embd : &m->wcls, r->xb, dim, m->vocab, r->logits)) return 1;
+    rec_op(rc, "linear_q4_0", NO_LAYER, rc ? (m->shared ? rc->tok : rc->wcls) : NULL, r->xb, dim, r->logits,
+           m->vocab);
+    rec_act(rc, tk, NO_LAYER, "post_lm_head", r->logits, m->vocab);
+    return 0;
 }
 
 /* argmax_last_dim (src/ops/argmax.rs:21-68): first maximum, strict > */
@@ -548,9 +635,9 @@ static void le32(uint8_t* o, uint32_t v) {
     o[3] = (uint8_t)(v >> 24);
 }
 
-int vtqo_run_quantized(const vtqo_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
-                       const uint32_t* prompt, int prompt_len, int n_new, int threads, float* logits,
-                       uint32_t* tokens, uint8_t digest[32], const char** msg) {
+static int run_impl(const vtqo_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
+                    const uint32_t* prompt, int prompt_len, int n_new, int threads, float* logits, uint32_t* tokens,
+                    rec_t* rec, uint8_t digest[32], const char** msg) {
     if (prompt_len == 0) {
         *msg = "prompt_tokens must not be empty";
         return 1;
@@ -564,6 +651,7 @@ int vtqo_run_quantized(const vtqo_model* m, int regime, const char* model_id, co
     run_t r;
     memset(&r, 0, sizeof r);
     r.m = m;
+    r.rec = rec;
     r.regime = regime;
     r.threads = threads < 1 ? 1 : threads;
     const size_t kv = (size_t)m->n_layers * m->seq_len * kv_dim;
@@ -616,7 +704,13 @@ int vtqo_run_quantized(const vtqo_model* m, int regime, const char* model_id, co
         const char* out_names[2] = {"output_tokens", "output_tokens_hash"};
         const uint8_t* out_data[2] = {ob, out_hash};
         const size_t out_lens[2] = {(size_t)n_new * 4, 32};
-        vtqo_digest_v2(5, in_names, in_data, in_lens, 2, out_names, out_data, out_lens, digest);
+        if (rec && rec->oom) {
+            *msg = "out of memory";
+            rc = 1;
+        } else {
+            vtqo_digest_v2_full(5, in_names, in_data, in_lens, 2, out_names, out_data, out_lens, rec ? rec->n_ops : 0,
+                                rec ? rec->ops : NULL, rec ? rec->n_acts : 0, rec ? rec->acts : NULL, digest);
+        }
         free(pb);
         free(ob);
     } else {
@@ -626,4 +720,58 @@ int vtqo_run_quantized(const vtqo_model* m, int regime, const char* model_id, co
     free(r.key_cache);
     free(r.value_cache);
     return rc;
+}
+
+int vtqo_run_quantized(const vtqo_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
+                       const uint32_t* prompt, int prompt_len, int n_new, int threads, float* logits,
+                       uint32_t* tokens, uint8_t digest[32], const char** msg) {
+    return run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, threads, logits, tokens, NULL,
+                    digest, msg);
+}
+
+/* PerOpRecorder::new (forward_quantized.rs:76-105): every weight hashed once */
+static void params_cache(const vtqo_model* m, rec_t* rc) {
+    vtqo_blake3_hash(m->tok_embd.w, m->tok_embd.len, rc->tok);
+    hash_f32(m->rms_final, (size_t)m->dim, rc->rms_final);
+    if (!m->shared) vtqo_blake3_hash(m->wcls.w, m->wcls.len, rc->wcls);
+    for (int l = 0; l < m->n_layers; l++) {
+        const layer_t* L = &m->layers[l];
+        hash_f32(L->rms_att, (size_t)m->dim, rc->params[l][0]);
+        vtqo_blake3_hash(L->wq.w, L->wq.len, rc->params[l][1]);
+        vtqo_blake3_hash(L->wk.w, L->wk.len, rc->params[l][2]);
+        vtqo_blake3_hash(L->wv.w, L->wv.len, rc->params[l][3]);
+        vtqo_blake3_hash(L->wo.w, L->wo.len, rc->params[l][4]);
+        hash_f32(L->rms_ffn, (size_t)m->dim, rc->params[l][5]);
+        vtqo_blake3_hash(L->w1.w, L->w1.len, rc->params[l][6]);
+        vtqo_blake3_hash(L->w2.w, L->w2.len, rc->params[l][7]);
+        vtqo_blake3_hash(L->w3.w, L->w3.len, rc->params[l][8]);
+    }
+}
+
+int vtqo_run_quantized_recorded(const vtqo_model* m, int regime, const char* model_id,
+                                const uint8_t weights_hash[32], const uint32_t* prompt, int prompt_len, int n_new,
+                                int threads, int flags, uint32_t* tokens, vtqo_op_record* ops, size_t ops_cap,
+                                vtqo_act_record* acts, size_t acts_cap, size_t* n_ops, size_t* n_acts,
+                                uint8_t digest[32], const char** msg) {
+    rec_t rc;
+    memset(&rc, 0, sizeof rc);
+    rc.flags = flags;
+    rc.params = (uint8_t(*)[9][32])calloc((size_t)(m->n_layers > 0 ? m->n_layers : 1), sizeof *rc.params);
+    if (!rc.params) {
+        *msg = "out of memory";
+        return 1;
+    }
+    if (flags & VTQO_RECORD_OPS) params_cache(m, &rc);
+    const int err = run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, threads, NULL, tokens, &rc,
+                             digest, msg);
+    if (!err) {
+        if (n_ops) *n_ops = rc.n_ops;
+        if (n_acts) *n_acts = rc.n_acts;
+        if (ops) memcpy(ops, rc.ops, (rc.n_ops < ops_cap ? rc.n_ops : ops_cap) * sizeof *ops);
+        if (acts) memcpy(acts, rc.acts, (rc.n_acts < acts_cap ? rc.n_acts : acts_cap) * sizeof *acts);
+    }
+    free(rc.ops);
+    free(rc.acts);
+    free(rc.params);
+    return err;
 }

@@ -77,6 +77,38 @@ int vtqo_run_quantized(const vtqo_model *m, int regime, const char *model_id, co
                        const uint32_t *prompt, int prompt_len, int n_new, int threads, float *logits,
                        uint32_t *tokens, uint8_t digest[32], const char **msg);
 
+/* PerOp / activation receipts (src/model/forward_quantized.rs:64-132,
+ * :260-284; src/cert/builder.rs:251-305, :489-560).  op_name is
+ * "rms_norm" or "linear_q4_0" (the reference's name for every linear);
+ * layer is 0xFFFFFFFF for the model-level ops and checkpoints. */
+#define VTQO_RECORD_OPS 1
+#define VTQO_RECORD_ACTIVATIONS 2
+typedef struct {
+    uint32_t op_index, layer;
+    char op_name[16];
+    uint8_t input_hash[32], params_hash[32], output_hash[32];
+} vtqo_op_record;
+typedef struct {
+    uint32_t act_index, token_index, layer;
+    char checkpoint[16];
+    uint8_t tensor_hash[32];
+} vtqo_act_record;
+
+/* compute_digest_v2 with op and activation sections (no interventions) */
+void vtqo_digest_v2_full(int n_in, const char *const *in_names, const uint8_t *const *in_data, const size_t *in_lens,
+                         int n_out, const char *const *out_names, const uint8_t *const *out_data,
+                         const size_t *out_lens, size_t n_ops, const vtqo_op_record *ops, size_t n_acts,
+                         const vtqo_act_record *acts, uint8_t out[32]);
+
+/* run_quantized's cert with a PerOpRecorder and/or a PerActivationRecorder
+ * attached to every step (flags: VTQO_RECORD_*).  ops / acts (optional)
+ * receive up to *_cap records; *n_ops / *n_acts the counts. */
+int vtqo_run_quantized_recorded(const vtqo_model *m, int regime, const char *model_id,
+                                const uint8_t weights_hash[32], const uint32_t *prompt, int prompt_len, int n_new,
+                                int threads, int flags, uint32_t *tokens, vtqo_op_record *ops, size_t ops_cap,
+                                vtqo_act_record *acts, size_t acts_cap, size_t *n_ops, size_t *n_acts,
+                                uint8_t digest[32], const char **msg);
+
 /* forward-step helpers, exported for their known-answer tests */
 void vtqo_rms_norm(const float* x, const float* w, int n, float eps, float* out);
 void vtqo_softmax(float* x, int n);

@@ -68,3 +68,35 @@ def test_e2e_config5_full_bit_exact():
     # Llama 1.1B shape, 128 prompt ids, 64 new tokens,
     # integer (std-parallel) regime; logits compared at all 192 steps
     compare(synth.LLAMA_1B1, synth.E2E_PROMPT, synth.E2E_NEW, regimes=(0,), threads=16)
+
+
+def compare_recorded(cfg, prompt_len, n_new, flags, regime=0):
+    blob, prompt = synth.e2e_inputs(cfg, prompt_len)
+    wh = bytes.fromhex(oracle.blake3(blob))
+    om = oracle.Model(blob)
+    gm = runtime.Model(blob)
+    try:
+        t_o, d_o, ops_o, acts_o = om.run_recorded(prompt, n_new, wh, flags=flags, regime=regime, threads=16)
+        t_g, d_g, ops_g, acts_g = gm.run_recorded(prompt, n_new, wh, flags=flags, regime=regime)
+    finally:
+        gm.close()
+    assert len(ops_g) == len(ops_o) and len(acts_g) == len(acts_o)
+    for a, b in zip(ops_g, ops_o):
+        assert a.key() == b.key(), f"op {b.op_index} ({b.op_name.decode()}, layer {b.layer}) differs"
+    for a, b in zip(acts_g, acts_o):
+        assert a.key() == b.key(), f"activation {b.act_index} ({b.checkpoint.decode()}, token {b.token_index}) differs"
+    assert np.array_equal(t_g, t_o) and d_g == d_o
+    return d_o
+
+
+def test_e2e_per_op_and_activation_receipts():
+    compare_recorded(SMALL, 5, 4, runtime.RECORD_OPS | runtime.RECORD_ACTIVATIONS)
+    compare_recorded(MEDIUM, 3, 6, runtime.RECORD_OPS, regime=1)
+    compare_recorded(MEDIUM, 2, 3, runtime.RECORD_ACTIVATIONS)
+
+
+def test_e2e_config5_receipts_bit_exact():
+    # config 5 with both recorders: 192 steps x 200 op records and 47 checkpoints
+    d = compare_recorded(synth.LLAMA_1B1, synth.E2E_PROMPT, synth.E2E_NEW,
+                         runtime.RECORD_OPS | runtime.RECORD_ACTIVATIONS)
+    assert len(d) == 64

@@ -122,3 +122,34 @@ def test_softmax_closed_forms():
     assert abs(float(y.sum()) - 1.0) < 1e-6 and y[1] > y[0]
     # the max is subtracted first: huge equal inputs do not overflow
     assert np.array_equal(oracle.softmax([1e30, 1e30]), np.array([0.5, 0.5], dtype=np.float32))
+
+
+def test_per_op_and_activation_receipts():
+    # perop_records_expected_count_and_matches_baseline_logits and
+    # perop_records_are_deterministic_across_runs (forward_quantized.rs:1235-1420):
+    # 9 ops per layer + 2 per step, the recorder only observes, and the same
+    # run gives the same records and digest
+    blob, prompt = synth.e2e_inputs(SMALL, 5)
+    wh = bytes.fromhex(oracle.blake3(blob))
+    m = oracle.Model(blob)
+    tokens, digest, _ = m.run(prompt, 3, wh, want_logits=False)
+    t1, d1, ops, acts = m.run_recorded(prompt, 3, wh)
+    steps, L = 8, SMALL["layers"]
+    assert np.array_equal(t1, tokens)
+    assert len(ops) == steps * (9 * L + 2) and len(acts) == steps * (2 * L + 3)
+    assert [o.op_index for o in ops] == list(range(len(ops)))
+    assert ops[0].op_name == b"rms_norm" and ops[1].op_name == b"linear_q4_0" and ops[0].layer == 0
+    assert ops[9 * L].layer == oracle.NO_LAYER and ops[9 * L + 1].op_name == b"linear_q4_0"
+    assert [a.checkpoint for a in acts[:2 * L + 3]] == [b"post_embed"] + [b"post_attn", b"post_ffn"] * L + \
+        [b"pre_lm_head", b"post_lm_head"]
+    assert acts[2 * L + 3].token_index == 1
+    # op inputs chain to the previous op's output where the reference feeds them
+    assert bytes(ops[1].input_hash) == bytes(ops[0].output_hash) == bytes(ops[2].input_hash)
+    # the records are bound into the digest; without recorders it is run_quantized's
+    assert d1 != digest
+    t2, d2, ops2, acts2 = m.run_recorded(prompt, 3, wh)
+    assert d2 == d1 and [o.key() for o in ops2] == [o.key() for o in ops]
+    _, d_ops, ops_only, acts_none = m.run_recorded(prompt, 3, wh, flags=oracle.RECORD_OPS)
+    assert acts_none == [] and len(ops_only) == len(ops) and d_ops not in (d1, digest)
+    _, d0, _, _ = m.run_recorded(prompt, 3, wh, flags=0)
+    assert d0 == digest

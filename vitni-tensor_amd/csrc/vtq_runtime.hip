@@ -28,8 +28,10 @@
 #include <cstdlib>
 #include <cstring>
 #include <algorithm>
+#include <array>
 #include <map>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/vtq.h"
@@ -279,6 +281,13 @@ struct vtqrt_model {
     size_t hist_cap = 0;
     uint32_t* tokens = nullptr;
     int* pos = nullptr;
+    // receipts: one step's recorded tensors (device and pinned host copies),
+    // and the weights' hashes (PerOpRecorder's params cache), built once
+    float *rec_dev = nullptr, *rec_host = nullptr;
+    size_t rec_cap = 0;
+    bool params_ready = false;
+    std::vector<std::array<uint8_t, 32>> params;  // [layer * 9 + k], k as in RecSlots
+    uint8_t tok_hash[32] = {}, rms_final_hash[32] = {}, wcls_hash[32] = {};
 };
 
 namespace {
@@ -427,6 +436,222 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
                      "argmax");
 }
 
+// ---- receipts (PerOpRecorder / PerActivationRecorder) ----
+
+// Float offsets of one step's recorded tensors in the record arena: per
+// layer the 14 tensors below, then the model-level ones.
+struct RecSlots {
+    enum { X_IN, XB, Q, K, V, ATT, XB2, POST_ATTN, XB_FFN, GATE, UP, FFN, XB_DOWN, POST_FFN, NL };
+    size_t off[NL] = {}, len[NL] = {}, per_layer = 0;
+    size_t post_embed = 0, x_pre_final = 0, x_final = 0, logits = 0, total = 0;
+    int layers = 0, dim = 0, vocab = 0;
+    explicit RecSlots(const vtqrt_model* m) {
+        const size_t D = m->dim, Kd = (size_t)m->kv_heads * (m->dim / m->heads), H = m->hidden;
+        const size_t lens[NL] = {D, D, D, Kd, Kd, D, D, D, D, H, H, H, D, D};
+        size_t o = 0;
+        for (int k = 0; k < NL; k++) {
+            off[k] = o;
+            len[k] = lens[k];
+            o += (lens[k] + 3) / 4 * 4;  // 16-byte aligned slots (q|k|v stay contiguous: D, Kd are multiples of 4)
+        }
+        per_layer = o;
+        layers = m->layers;
+        dim = m->dim;
+        vocab = m->vocab;
+        post_embed = (size_t)layers * per_layer;
+        x_pre_final = post_embed + (D + 3) / 4 * 4;
+        x_final = x_pre_final + (D + 3) / 4 * 4;
+        logits = x_final + (D + 3) / 4 * 4;
+        total = logits + ((size_t)m->vocab + 3) / 4 * 4;
+    }
+    size_t at(int l, int k) const { return (size_t)l * per_layer + off[k]; }
+};
+
+int dcopy(vtqrt_model* m, float* dst, const float* src, int n) {
+    return hip_check(m, hipMemcpyAsync(dst, src, (size_t)n * 4, hipMemcpyDeviceToDevice, m->stream), "record copy");
+}
+
+// step_with_recorders: the unfused step with every recorded tensor written
+// to (or copied into) the record arena A
+int enqueue_step_recorded(vtqrt_model* m, int regime, int prompt_len, int total, float* A) {
+    namespace dec = vtq::decode;
+    const RecSlots S(m);
+    const int dim = m->dim, head = dim / m->heads, kv_dim = m->kv_heads * head, hidden = m->hidden;
+    int rc = dcopy(m, A + S.post_embed, m->x, dim);
+    for (int l = 0; !rc && l < m->layers; l++) {
+        const Layer& Ly = m->L[l];
+        float* R[RecSlots::NL];
+        for (int k = 0; k < RecSlots::NL; k++) R[k] = A + S.at(l, k);
+        if ((rc = dcopy(m, R[RecSlots::X_IN], m->x, dim))) break;
+        if ((rc = hip_check(m, dec::rms_norm(m->x, f32_at(m, Ly.rms_att), dim, m->eps, R[RecSlots::XB], m->stream),
+                            "rms_norm")))
+            break;
+        if ((rc = linear(m, regime, Ly.wq, R[RecSlots::XB], dim, dim, R[RecSlots::Q])) ||
+            (rc = linear(m, regime, Ly.wk, R[RecSlots::XB], dim, kv_dim, R[RecSlots::K])) ||
+            (rc = linear(m, regime, Ly.wv, R[RecSlots::XB], dim, kv_dim, R[RecSlots::V])))
+            break;
+        dec::AttnArgs a;
+        a.qkv = R[RecSlots::Q];
+        a.bq = f32_at(m, Ly.bq);
+        a.bk = f32_at(m, Ly.bk);
+        a.bv = f32_at(m, Ly.bv);
+        a.kc = m->kc + (size_t)l * m->seq * kv_dim;
+        a.vc = m->vc + (size_t)l * m->seq * kv_dim;
+        a.cs = m->rope;
+        a.out = R[RecSlots::ATT];
+        a.pos = m->pos;
+        a.heads = m->heads;
+        a.kv_heads = m->kv_heads;
+        a.head_dim = head;
+        a.seq = m->seq;
+        a.theta = m->theta;
+        a.neox = m->neox ? 1 : 0;
+        if ((rc = hip_check(m, dec::attention(a, m->stream), "attention"))) break;
+        if ((rc = linear(m, regime, Ly.wo, R[RecSlots::ATT], dim, dim, R[RecSlots::XB2])) ||
+            (rc = hip_check(m, dec::add_inplace(m->x, R[RecSlots::XB2], dim, m->stream), "residual")) ||
+            (rc = dcopy(m, R[RecSlots::POST_ATTN], m->x, dim)))
+            break;
+        if ((rc = hip_check(m, dec::rms_norm(m->x, f32_at(m, Ly.rms_ffn), dim, m->eps, R[RecSlots::XB_FFN], m->stream),
+                            "rms_norm")))
+            break;
+        if ((rc = linear(m, regime, Ly.w1, R[RecSlots::XB_FFN], dim, hidden, R[RecSlots::GATE])) ||
+            (rc = linear(m, regime, Ly.w3, R[RecSlots::XB_FFN], dim, hidden, R[RecSlots::UP])) ||
+            (rc = hip_check(m, dec::swiglu(R[RecSlots::GATE], R[RecSlots::UP], R[RecSlots::FFN], hidden, m->stream),
+                            "swiglu")) ||
+            (rc = linear(m, regime, Ly.w2, R[RecSlots::FFN], hidden, dim, R[RecSlots::XB_DOWN])) ||
+            (rc = hip_check(m, dec::add_inplace(m->x, R[RecSlots::XB_DOWN], dim, m->stream), "residual")) ||
+            (rc = dcopy(m, R[RecSlots::POST_FFN], m->x, dim)))
+            break;
+    }
+    if (rc) return rc;
+    const Lin& head_w = m->shared ? m->tok : m->wcls;
+    if ((rc = dcopy(m, A + S.x_pre_final, m->x, dim)) ||
+        (rc = hip_check(m, dec::rms_norm(m->x, f32_at(m, m->rms_final), dim, m->eps, A + S.x_final, m->stream),
+                        "rms_norm")) ||
+        (rc = linear(m, regime, head_w, A + S.x_final, dim, m->vocab, A + S.logits)))
+        return rc;
+    return hip_check(m, dec::argmax_advance(A + S.logits, m->vocab, m->tokens, m->pos, prompt_len, total, nullptr,
+                                            embed_args(m), m->stream),
+                     "argmax");
+}
+
+// fn(i) for i in [0, n) on up to 16 threads (the items are independent)
+template <class F>
+void parallel_for(int n, F fn) {
+    const unsigned hw = std::thread::hardware_concurrency();
+    const int t = std::max(1, std::min({n, 16, (int)(hw ? hw : 1)}));
+    std::vector<std::thread> th;
+    for (int w = 1; w < t; w++)
+        th.emplace_back([&, w] {
+            for (int i = w; i < n; i += t) fn(i);
+        });
+    for (int i = 0; i < n; i += t) fn(i);
+    for (auto& x : th) x.join();
+}
+
+// PerOpRecorder::new (forward_quantized.rs:76-105): BLAKE3 of every weight
+// tensor's bytes, hash_f32_slice of every norm
+void build_params(vtqrt_model* m) {
+    if (m->params_ready) return;
+    const uint8_t* b = m->blob.data();
+    m->params.assign((size_t)m->layers * 9, {});
+    auto lin_hash = [&](const Lin& w, uint8_t* out) { vtqrt_blake3(b + w.offset, w.nbytes, out); };
+    auto f32_hash = [&](size_t off, uint8_t* out) { vtqrt_blake3(b + off, (size_t)m->dim * 4, out); };
+    parallel_for(m->layers * 9 + 3, [&](int i) {
+        if (i == m->layers * 9) return lin_hash(m->tok, m->tok_hash);
+        if (i == m->layers * 9 + 1) return f32_hash(m->rms_final, m->rms_final_hash);
+        if (i == m->layers * 9 + 2) {
+            if (!m->shared) lin_hash(m->wcls, m->wcls_hash);
+            return;
+        }
+        const Layer& Ly = m->L[i / 9];
+        uint8_t* o = m->params[i].data();
+        switch (i % 9) {
+        case 0: return f32_hash(Ly.rms_att, o);
+        case 1: return lin_hash(Ly.wq, o);
+        case 2: return lin_hash(Ly.wk, o);
+        case 3: return lin_hash(Ly.wv, o);
+        case 4: return lin_hash(Ly.wo, o);
+        case 5: return f32_hash(Ly.rms_ffn, o);
+        case 6: return lin_hash(Ly.w1, o);
+        case 7: return lin_hash(Ly.w2, o);
+        default: return lin_hash(Ly.w3, o);
+        }
+    });
+    m->params_ready = true;
+}
+
+struct Recorder {
+    int flags = 0;
+    std::vector<vtqrt_op_record> ops;
+    std::vector<vtqrt_act_record> acts;
+};
+
+// hash one step's recorded tensors (host copy H) and append the step's
+// records in the reference's declaration order
+void record_step(vtqrt_model* m, Recorder& rec, const float* H, uint32_t token) {
+    const RecSlots S(m);
+    const int NL = RecSlots::NL, L = m->layers;
+    const uint32_t kNoLayer = 0xFFFFFFFFu;
+    std::vector<std::array<uint8_t, 32>> h((size_t)L * NL + 4);
+    parallel_for((int)h.size(), [&](int i) {
+        size_t off, n;
+        if (i < L * NL) {
+            off = S.at(i / NL, i % NL);
+            n = S.len[i % NL];
+        } else {
+            const int j = i - L * NL;
+            off = j == 0 ? S.post_embed : j == 1 ? S.x_pre_final : j == 2 ? S.x_final : S.logits;
+            n = j == 3 ? (size_t)m->vocab : (size_t)m->dim;
+        }
+        vtqrt_blake3(H + off, n * 4, h[i].data());
+    });
+    auto H_ = [&](int l, int k) { return h[(size_t)l * NL + k].data(); };
+    const uint8_t *post_embed = h[(size_t)L * NL].data(), *pre_final = h[(size_t)L * NL + 1].data(),
+                  *x_final = h[(size_t)L * NL + 2].data(), *logits = h[(size_t)L * NL + 3].data();
+    auto op = [&](const char* name, uint32_t layer, const uint8_t* params, const uint8_t* in, const uint8_t* out) {
+        if (!(rec.flags & VTQRT_RECORD_OPS)) return;
+        vtqrt_op_record r{};
+        r.op_index = (uint32_t)rec.ops.size();
+        r.layer = layer;
+        std::strncpy(r.op_name, name, sizeof r.op_name - 1);
+        std::memcpy(r.input_hash, in, 32);
+        if (params) std::memcpy(r.params_hash, params, 32);
+        std::memcpy(r.output_hash, out, 32);
+        rec.ops.push_back(r);
+    };
+    auto act = [&](uint32_t layer, const char* cp, const uint8_t* t) {
+        if (!(rec.flags & VTQRT_RECORD_ACTIVATIONS)) return;
+        vtqrt_act_record r{};
+        r.act_index = (uint32_t)rec.acts.size();
+        r.token_index = token;
+        r.layer = layer;
+        std::strncpy(r.checkpoint, cp, sizeof r.checkpoint - 1);
+        std::memcpy(r.tensor_hash, t, 32);
+        rec.acts.push_back(r);
+    };
+    act(kNoLayer, "post_embed", post_embed);
+    for (int l = 0; l < L; l++) {
+        const auto P = [&](int k) { return m->params[(size_t)l * 9 + k].data(); };
+        using RS = RecSlots;
+        op("rms_norm", l, P(0), H_(l, RS::X_IN), H_(l, RS::XB));
+        op("linear_q4_0", l, P(1), H_(l, RS::XB), H_(l, RS::Q));
+        op("linear_q4_0", l, P(2), H_(l, RS::XB), H_(l, RS::K));
+        op("linear_q4_0", l, P(3), H_(l, RS::XB), H_(l, RS::V));
+        op("linear_q4_0", l, P(4), H_(l, RS::ATT), H_(l, RS::XB2));
+        act(l, "post_attn", H_(l, RS::POST_ATTN));
+        op("rms_norm", l, P(5), H_(l, RS::POST_ATTN), H_(l, RS::XB_FFN));
+        op("linear_q4_0", l, P(6), H_(l, RS::XB_FFN), H_(l, RS::GATE));
+        op("linear_q4_0", l, P(8), H_(l, RS::XB_FFN), H_(l, RS::UP));
+        op("linear_q4_0", l, P(7), H_(l, RS::FFN), H_(l, RS::XB_DOWN));
+        act(l, "post_ffn", H_(l, RS::POST_FFN));
+    }
+    op("rms_norm", kNoLayer, m->rms_final_hash, pre_final, x_final);
+    act(kNoLayer, "pre_lm_head", x_final);
+    op("linear_q4_0", kNoLayer, m->shared ? m->tok_hash : m->wcls_hash, x_final, logits);
+    act(kNoLayer, "post_lm_head", logits);
+}
+
 const Meta* meta(const std::map<std::string, Meta>& kv, const std::string& k) {
     auto it = kv.find(k);
     return it == kv.end() ? nullptr : &it->second;
@@ -475,6 +700,8 @@ void vtqrt_free(vtqrt_model* m) {
                     (void*)m->gate, (void*)m->up, (void*)m->tmp, (void*)m->logits, (void*)m->kc, (void*)m->vc,
                     (void*)m->hist, (void*)m->tokens, (void*)m->pos, (void*)m->rope})
         if (p) (void)hipFree(p);
+    if (m->rec_dev) (void)hipFree(m->rec_dev);
+    if (m->rec_host) (void)hipHostFree(m->rec_host);
     if (m->stream) (void)hipStreamDestroy(m->stream);
     if (m->ctx) vtq_destroy(m->ctx);
     delete m;
@@ -640,9 +867,13 @@ int vtqrt_load(int device, const uint8_t* gguf, size_t len, vtqrt_model** out) {
     return VTQ_OK;
 }
 
-int vtqrt_run(vtqrt_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
-              const uint32_t* prompt, int prompt_len, int n_new, float* logits, uint32_t* tokens,
-              uint8_t digest[32]) {
+}  // extern "C"
+
+namespace {
+
+// run_quantized (inference.rs:274-345), optionally with the step recorders
+int run_impl(vtqrt_model* m, int regime, const char* model_id, const uint8_t weights_hash[32], const uint32_t* prompt,
+             int prompt_len, int n_new, float* logits, uint32_t* tokens, uint8_t digest[32], Recorder* rec) {
     if (!m || !m->ctx || !model_id || !weights_hash || !digest || (prompt_len > 0 && !prompt) ||
         (n_new > 0 && !tokens) || n_new < 0)
         return VTQ_E_INVALID_ARGUMENT;
@@ -667,6 +898,25 @@ int vtqrt_run(vtqrt_model* m, int regime, const char* model_id, const uint8_t we
         m->hist_cap = (size_t)total * m->vocab;
     }
     float* hist = logits ? m->hist : nullptr;
+    if (rec) {
+        build_params(m);
+        const RecSlots S(m);
+        if (m->rec_cap < S.total) {
+            if (m->rec_dev) (void)hipFree(m->rec_dev);
+            if (m->rec_host) (void)hipHostFree(m->rec_host);
+            m->rec_dev = m->rec_host = nullptr;
+            m->rec_cap = 0;
+            if ((rc = hip_check(m, hipMalloc(&m->rec_dev, S.total * 4), "hipMalloc(records)")) ||
+                (rc = hip_check(m, hipHostMalloc(&m->rec_host, S.total * 4, hipHostMallocDefault),
+                                "hipHostMalloc(records)")))
+                return rc;
+            m->rec_cap = S.total;
+        }
+    }
+    auto enqueue = [&]() {
+        return rec ? enqueue_step_recorded(m, regime, prompt_len, total, m->rec_dev)
+                   : enqueue_step(m, regime, prompt_len, total, hist);
+    };
     // tokens[0 .. prompt_len) = prompt; step p reads tokens[p] and its argmax
     // writes tokens[p + 1] once p + 1 >= prompt_len
     const int zero = 0;
@@ -682,7 +932,7 @@ int vtqrt_run(vtqrt_model* m, int regime, const char* model_id, const uint8_t we
     const char* eager_env = std::getenv("VTQRT_EAGER");
     if (!(eager_env && *eager_env && *eager_env != '0') &&
         hipStreamBeginCapture(m->stream, hipStreamCaptureModeRelaxed) == hipSuccess) {
-        const int crc = enqueue_step(m, regime, prompt_len, total, hist);
+        const int crc = enqueue();
         const hipError_t ce = hipStreamEndCapture(m->stream, &graph);
         if (crc || ce != hipSuccess || !graph || hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
             if (exec) (void)hipGraphExecDestroy(exec);
@@ -695,9 +945,17 @@ int vtqrt_run(vtqrt_model* m, int regime, const char* model_id, const uint8_t we
     rc = hip_check(m, vtq::decode::embed(m->tok.type, m->dblob + m->tok.offset, table_rows(m), m->tokens, m->pos, m->dim,
                                          m->x, rope_args(m), m->stream),
                    "embedding_row");
-    for (int pos = 0; pos < total && !rc; pos++)
-        rc = exec ? hip_check(m, hipGraphLaunch(exec, m->stream), "hipGraphLaunch")
-                  : enqueue_step(m, regime, prompt_len, total, hist);
+    for (int pos = 0; pos < total && !rc; pos++) {
+        rc = exec ? hip_check(m, hipGraphLaunch(exec, m->stream), "hipGraphLaunch") : enqueue();
+        if (!rc && rec) {
+            // this step's recorded tensors to the host, hashed there
+            const RecSlots S(m);
+            rc = hip_check(m, hipMemcpyAsync(m->rec_host, m->rec_dev, S.total * 4, hipMemcpyDeviceToHost, m->stream),
+                           "hipMemcpyAsync(records)");
+            if (!rc) rc = hip_check(m, hipStreamSynchronize(m->stream), "hipStreamSynchronize");
+            if (!rc) record_step(m, *rec, m->rec_host, (uint32_t)pos);
+        }
+    }
     if (exec) (void)hipGraphExecDestroy(exec);
     if (rc) {
         (void)hipStreamSynchronize(m->stream);
@@ -753,10 +1011,60 @@ int vtqrt_run(vtqrt_model* m, int regime, const char* model_id, const uint8_t we
     leb128(h, 2);
     field("output_tokens", ob.data(), ob.size());
     field("output_tokens_hash", out_hash, 32);
-    leb128(h, 0);
-    leb128(h, 0);
+    // ops and activations (write_op / write_activation, builder.rs:525-560); no interventions
+    const size_t n_ops = rec ? rec->ops.size() : 0, n_acts = rec ? rec->acts.size() : 0;
+    leb128(h, n_ops);
+    for (size_t i = 0; i < n_ops; i++) {
+        const vtqrt_op_record& o = rec->ops[i];
+        const size_t nl = std::strlen(o.op_name);
+        leb128(h, o.op_index);
+        leb128(h, nl);
+        h.update(o.op_name, nl);
+        leb128(h, o.layer);
+        h.update(o.input_hash, 32);
+        h.update(o.params_hash, 32);
+        h.update(o.output_hash, 32);
+    }
+    leb128(h, n_acts);
+    for (size_t i = 0; i < n_acts; i++) {
+        const vtqrt_act_record& a = rec->acts[i];
+        const size_t nl = std::strlen(a.checkpoint);
+        leb128(h, a.act_index);
+        leb128(h, a.token_index);
+        leb128(h, a.layer);
+        leb128(h, nl);
+        h.update(a.checkpoint, nl);
+        h.update(a.tensor_hash, 32);
+    }
     leb128(h, 0);
     h.final(digest);
+    return VTQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vtqrt_run(vtqrt_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
+              const uint32_t* prompt, int prompt_len, int n_new, float* logits, uint32_t* tokens,
+              uint8_t digest[32]) {
+    return run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, logits, tokens, digest, nullptr);
+}
+
+int vtqrt_run_recorded(vtqrt_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
+                       const uint32_t* prompt, int prompt_len, int n_new, int flags, uint32_t* tokens,
+                       vtqrt_op_record* ops, size_t ops_cap, vtqrt_act_record* acts, size_t acts_cap,
+                       size_t* n_ops, size_t* n_acts, uint8_t digest[32]) {
+    if (flags & ~(VTQRT_RECORD_OPS | VTQRT_RECORD_ACTIVATIONS)) return VTQ_E_INVALID_ARGUMENT;
+    Recorder rec;
+    rec.flags = flags;
+    const int rc = run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, nullptr, tokens, digest,
+                            &rec);
+    if (rc) return rc;
+    if (n_ops) *n_ops = rec.ops.size();
+    if (n_acts) *n_acts = rec.acts.size();
+    if (ops) std::memcpy(ops, rec.ops.data(), std::min(ops_cap, rec.ops.size()) * sizeof *ops);
+    if (acts) std::memcpy(acts, rec.acts.data(), std::min(acts_cap, rec.acts.size()) * sizeof *acts);
     return VTQ_OK;
 }
 

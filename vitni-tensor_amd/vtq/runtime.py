@@ -32,6 +32,9 @@ def lib() -> ctypes.CDLL:
         L.vtqrt_dims.restype = i
         L.vtqrt_run.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, vp, vp, vp]
         L.vtqrt_run.restype = i
+        L.vtqrt_run_recorded.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, i, vp, vp, sz, vp, sz,
+                                         ctypes.POINTER(sz), ctypes.POINTER(sz), vp]
+        L.vtqrt_run_recorded.restype = i
         L.vtqrt_blake3.argtypes = [vp, sz, vp]
         L.vtqrt_blake3.restype = None
         _rt = L
@@ -44,6 +47,30 @@ def blake3(data) -> bytes:
     out = (ctypes.c_uint8 * 32)()
     lib().vtqrt_blake3(d.ctypes.data if d.size else None, d.size, out)
     return bytes(out)
+
+
+RECORD_OPS = 1
+RECORD_ACTIVATIONS = 2
+
+
+class OpRecord(ctypes.Structure):
+    """vtqrt_op_record: one PerOp receipt entry."""
+    _fields_ = [("op_index", ctypes.c_uint32), ("layer", ctypes.c_uint32), ("op_name", ctypes.c_char * 16),
+                ("input_hash", ctypes.c_uint8 * 32), ("params_hash", ctypes.c_uint8 * 32),
+                ("output_hash", ctypes.c_uint8 * 32)]
+
+    def key(self):
+        return (self.op_index, self.layer, self.op_name, bytes(self.input_hash), bytes(self.params_hash),
+                bytes(self.output_hash))
+
+
+class ActRecord(ctypes.Structure):
+    """vtqrt_act_record: one activation-checkpoint receipt entry."""
+    _fields_ = [("act_index", ctypes.c_uint32), ("token_index", ctypes.c_uint32), ("layer", ctypes.c_uint32),
+                ("checkpoint", ctypes.c_char * 16), ("tensor_hash", ctypes.c_uint8 * 32)]
+
+    def key(self):
+        return (self.act_index, self.token_index, self.layer, self.checkpoint, bytes(self.tensor_hash))
 
 
 class Model:
@@ -76,6 +103,25 @@ class Model:
         if logits is not None:
             logits = logits.reshape(prompt.size + n_new, self.vocab)
         return tokens[:n_new], bytes(digest).hex(), logits
+
+    def run_recorded(self, prompt, n_new, weights_hash: bytes, flags=RECORD_OPS | RECORD_ACTIVATIONS, regime=0,
+                     model_id="vitni-receipt"):
+        """run_quantized with per-op / activation receipts:
+        (generated tokens, v2 digest hex, [OpRecord], [ActRecord])."""
+        prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
+        wh = np.frombuffer(bytes(weights_hash), dtype=np.uint8).copy()
+        tokens = np.zeros(max(1, n_new), dtype=np.uint32)
+        steps = prompt.size + n_new
+        ops = (OpRecord * max(1, steps * (9 * self.layers + 2)))()
+        acts = (ActRecord * max(1, steps * (2 * self.layers + 3)))()
+        n_ops, n_acts = ctypes.c_size_t(), ctypes.c_size_t()
+        digest = (ctypes.c_uint8 * 32)()
+        rc = lib().vtqrt_run_recorded(self.handle, regime, model_id.encode(), wh.ctypes.data, prompt.ctypes.data,
+                                      prompt.size, n_new, flags, tokens.ctypes.data, ops, len(ops), acts, len(acts),
+                                      ctypes.byref(n_ops), ctypes.byref(n_acts), digest)
+        if rc:
+            raise _ERR.get(rc, GpuError)(lib().vtqrt_last_error(self.handle).decode())
+        return tokens[:n_new], bytes(digest).hex(), list(ops[:n_ops.value]), list(acts[:n_acts.value])
 
     def close(self):
         if self.handle:
