@@ -20,18 +20,26 @@
 namespace vtq {
 
 constexpr int kChunk = 8192;
+// Raw buffer descriptor word 3 (untyped, stride 0) on gfx9-family parts, and
+// an offset past every buffer the windowed kernel builds (each < 2 GiB):
+// loads there return zeros without touching memory.
+constexpr int kPcBufferWord3 = 0x00020000;
+constexpr uint32_t kPcOutOfRange = 0x80000000u;
 constexpr int kMaxChunkSlots = 8;  // in_feat <= 65536
 
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) { return *reinterpret_cast<const uint16_t*>(p); }
 
 // Each decoder yields the weights of lane j's elements of one block:
-// elements kBlock*bi + j + 8m, m = 0 .. kBlock/8 - 1.
+// elements kBlock*bi + j + 8m, m = 0 .. kBlock/8 - 1.  Scales go through the
+// hardware f16 conversion, exact for every non-NaN code; a NaN comes out
+// quieted, and since every decoded scale is multiplied before use (which
+// quiets a NaN anyway), the weights and products are unchanged.
 struct DecQ8_0 {  // src/ops/quant.rs:193-210
     static constexpr int kBlock = 32;
     static constexpr int kWinBytes = 8 * 34;  // bytes of 256 elements
     __device__ static void decode(const uint8_t* row, int bi, int j, float* w) {
         const uint8_t* blk = row + 34 * bi;
-        const float d = f16_to_f32_sel(ld_u16(blk));
+        const float d = f16_hw(ld_u16(blk));
 #pragma unroll
         for (int m = 0; m < 4; m++) w[m] = d * (float)(int8_t)blk[2 + j + 8 * m];
     }
@@ -42,7 +50,7 @@ struct DecQ5_0 {  // src/ops/quant.rs:160-186
     static constexpr int kWinBytes = 8 * 22;
     __device__ static void decode(const uint8_t* row, int bi, int j, float* w) {
         const uint8_t* blk = row + 22 * bi;
-        const float d = f16_to_f32_sel(ld_u16(blk));
+        const float d = f16_hw(ld_u16(blk));
         const uint32_t qh = ld_u16(blk + 2) | (ld_u16(blk + 4) << 16);
         const uint8_t* qs = blk + 6;
 #pragma unroll
@@ -60,7 +68,7 @@ struct DecQ4_0 {  // src/ops/quant.rs:91-111 (element 2k low nibble, 2k+1 high)
     static constexpr int kWinBytes = 8 * 18;
     __device__ static void decode(const uint8_t* row, int bi, int j, float* w) {
         const uint8_t* blk = row + 18 * bi;
-        const float d = f16_to_f32_sel(ld_u16(blk));
+        const float d = f16_hw(ld_u16(blk));
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const int e = j + 8 * m;
@@ -77,8 +85,8 @@ struct DecQ4KFloat {  // src/ops/quant.rs:649-667: w = d1*q - m1f per sub-block
     __device__ static void decode(const uint8_t* row, int bi, int j, float* w) {
         const int sb = bi >> 3, sj = bi & 7;
         const uint8_t* blk = row + 144 * sb;
-        const float d = f16_to_f32_sel(ld_u16(blk));
-        const float dmin = f16_to_f32_sel(ld_u16(blk + 2));
+        const float d = f16_hw(ld_u16(blk));
+        const float dmin = f16_hw(ld_u16(blk + 2));
         const uint8_t* s = blk + 4;
         uint32_t sc, mn;
         if (sj < 4) {
@@ -162,20 +170,24 @@ __global__ __launch_bounds__(256) void canon_gemv_kernel(const float* __restrict
 // Products of elements past a chunk's end are written as -0.0, which is the
 // exact additive identity, so every chain adds 32 values per window.  One
 // barrier per window; LDS buffers alternate by window parity.  All loads
-// are unconditional (clamped past the end), so the wait counts stay exact.
-// Weight chunks may read up to 15 bytes past the end of the blob, within
-// the caller's 16-byte-rounded allocation.
+// are unconditional buffer loads (past a buffer's end they read zeros), so
+// the wait counts stay exact.  Weight chunks may read up to 15 bytes past
+// the end of the blob, within the caller's 16-byte-rounded allocation.
+// In full windows of live rows the products need no -0.0 masking, and that
+// test is skipped.
 template <class Dec, int CPW>
 struct PcWin {
     static constexpr int kRows = 8 / CPW;
     static constexpr int WB = Dec::kWinBytes;         // a multiple of 16 for every format
     static constexpr int RAWB = (WB + 30) / 16 * 16;  // window + misalignment slack, whole chunks
     static constexpr int NCH = RAWB / 16;             // 16-byte chunks per group window
-    static constexpr int NLOAD = 8 * NCH + 64 * CPW;  // chunks per window: weights, then x
+    static constexpr int XCH = 64 * CPW;              // x chunks per window: the first CPW producer waves
+    static constexpr int NLOAD = 8 * NCH + XCH;       // chunks per window: x, then weights
     static constexpr int NPW = 8;                     // producer waves
     static constexpr int NP = 64 * NPW;               // producer lanes
     static constexpr int UPL = 512 / NP;              // product units per producer lane
     static constexpr int LPL = (NLOAD + NP - 1) / NP;  // chunk loads per producer lane
+    static constexpr int NS = 4;                      // register slots: windows in flight beyond the staged one
     static constexpr int XS = 36;                     // chain stride (floats) of x and product windows
     static constexpr int GS = 8 * XS;                 // group stride of the product window
     static constexpr int EPB = Dec::kBlock / 8;       // chain elements per block
@@ -186,15 +198,15 @@ struct PcWin {
 
     // per producer lane, fixed for the whole row walk
     struct Chunk {             // one 16-byte fetch per window
-        const uint8_t* base;   // address at window 0
-        int cap;               // last window index it may advance to
-        int step;              // bytes per window (weights) or 0 for x
+        uint32_t off;          // buffer offset at window 0 (out of range: a dead slot, reads zeros)
+        uint32_t step;         // bytes per window
         int dst;               // LDS byte offset: raw, x (-1 - transposed slot) or spare
     };
     struct Unit {              // 4 consecutive chain positions of one group
         int raw, xoff, poff;   // LDS offsets: block bytes of the group, x quad, product quad
         int e0, ce;            // element of position 0 at window 0, chunk end
         int blk, j;            // block index in the window (f32: first of 4), chain
+        int full;              // windows whose 4 positions are all live (0: a dead slot)
         bool live;
     };
 };
@@ -220,7 +232,7 @@ __global__ __launch_bounds__(576) void canon_pc_kernel(const float* __restrict__
     const float* xb = x + (size_t)blockIdx.y * n;
 
     // Step i: producers form window i's products and stage window i+1 (from
-    // register slot r, refilled with window i+5); the consumer adds window
+    // register slot r, refilled with window i+1+NS); the consumer adds window
     // i-1's products.  Buffers alternate by window parity.  The two roles run
     // separate loops with the same barrier sequence, so the producers'
     // register slots never merge with the consumer's path.
@@ -230,7 +242,7 @@ __global__ __launch_bounds__(576) void canon_pc_kernel(const float* __restrict__
         const int o = row0 + u / CPW;
         float acc = (o < out_feat && c < nchunks) ? 0.0f : -0.0f;  // -0.0: padding slot past the row's end
         __syncthreads();
-        for (int i = 0; i <= nwin || (i & 3) != 0; i++) {
+        for (int i = 0; i <= nwin || (i % Wn::NS) != 0; i++) {
             if (i >= 1 && i <= nwin) {
                 const float* pp = prod_of((i & 1) ^ 1) + u * GS + j * XS;
                 float4 v[8];
@@ -253,32 +265,41 @@ __global__ __launch_bounds__(576) void canon_pc_kernel(const float* __restrict__
     }
 
     // ---- producers
+    // Chunk q of a window: q < 64 * CPW are x chunks, loaded by the first CPW
+    // producer waves, then 8 * NCH weight chunks, then spare lanes.  Weights
+    // are read through one buffer over this workgroup's rows (16-byte aligned
+    // start, end rounded up to 16 bytes, which the caller keeps readable) and
+    // x through one over this batch row: a fetch past a row's end reads the
+    // next row or zeros, never outside the buffers, so no address is clamped.
     const int pl = tid - 64;
-    const uint8_t* wlast = W + ((wbytes - 1) & ~(size_t)15);  // chunk holding the blob's last byte
-    const int last_win = (n - 1) / 256;
+    const int pw = __builtin_amdgcn_readfirstlane(pl >> 6);  // producer wave (uniform)
+    constexpr int XCH = Wn::XCH;
+    const size_t wg0 = ((size_t)row0 * row_bytes) & ~(size_t)15;
+    const size_t wg1 = (min(wbytes, (size_t)(row0 + Wn::kRows) * row_bytes) + 15) & ~(size_t)15;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W + wg0), (short)0,
+                                                                        (int)(wg1 - wg0), kPcBufferWord3);
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(xb), (short)0, 4 * n,
+                                                                        kPcBufferWord3);
     typename Wn::Chunk ch[LPL];
 #pragma unroll
     for (int k = 0; k < LPL; k++) {
         const int q = pl + NP * k;
-        if (q < 8 * NCH) {
-            const int g = q / NCH;
-            const int og = min(row0 + g / CPW, out_feat - 1), cg = min(g % CPW, nchunks - 1);
-            const size_t b0 = (size_t)og * row_bytes + (size_t)cg * (kChunk / 256) * WB;  // window 0 of the chunk
-            ch[k].base = W + (b0 & ~(size_t)15) + 16 * (q % NCH);
-            ch[k].cap = min(nwin - 1, last_win - cg * (kChunk / 256));
-            ch[k].step = WB;
-            ch[k].dst = g * RAWB + 16 * (q % NCH);
-        } else if (q < NLOAD) {
-            const int xi = q - 8 * NCH, s2 = xi >> 6, xl = xi & 63;
-            const int cs2 = min(s2, nchunks - 1) * kChunk;
-            ch[k].base = reinterpret_cast<const uint8_t*>(xb + cs2 + 4 * xl);
-            // x windows of the chunk, clamped so the float4 stays inside x
-            ch[k].cap = min(nwin - 1, (n - 4 - cs2 - 4 * xl) / 256);
+        ch[k].off = kPcOutOfRange;
+        if (k == 0 && pw < CPW) {
+            const int s2 = q >> 6, xl = q & 63;
+            if (s2 < nchunks) ch[k].off = 4u * (uint32_t)(s2 * kChunk + 4 * xl);
             ch[k].step = 1024;
             ch[k].dst = -1 - (s2 * GS + (4 * (xl & 1)) * XS + (xl >> 1));  // x element 4*xl+i: chain 4*(xl&1)+i
+        } else if (q < NLOAD) {
+            const int qw = q - XCH, g = qw / NCH;
+            const int og = row0 + g / CPW, cg = g % CPW;
+            if (og < out_feat && cg < nchunks) {
+                const size_t b0 = (size_t)og * row_bytes + (size_t)cg * (kChunk / 256) * WB;  // window 0 of the chunk
+                ch[k].off = (uint32_t)((b0 & ~(size_t)15) - wg0) + 16u * (uint32_t)(qw % NCH);
+            }
+            ch[k].step = WB;
+            ch[k].dst = g * RAWB + 16 * (qw % NCH);
         } else {
-            ch[k].base = reinterpret_cast<const uint8_t*>(xb);
-            ch[k].cap = 0;
             ch[k].step = 0;
             ch[k].dst = kRawBytes + kXsBytes + kProdBytes;  // marks the spare slot
         }
@@ -298,14 +319,17 @@ __global__ __launch_bounds__(576) void canon_pc_kernel(const float* __restrict__
         un[k2].blk = EPB == 4 ? t : 4 * t;
         un[k2].j = j;
         un[k2].live = og < out_feat && cg < nchunks;
+        // position m of window w is element e0 + 256 w + 8 m
+        un[k2].full = un[k2].live ? max(0, (un[k2].ce - un[k2].e0 - 24 + 255) / 256) : 0;
     }
 
     auto load = [&](int w) __attribute__((always_inline)) -> typename Wn::Regs {
         typename Wn::Regs r;
 #pragma unroll
         for (int k = 0; k < LPL; k++) {
-            const uint8_t* a = ch[k].base + (size_t)min(w, ch[k].cap) * ch[k].step;
-            const uint4 v = *reinterpret_cast<const uint4*>(a < wlast || ch[k].step != WB ? a : wlast);
+            const __amdgpu_buffer_rsrc_t rs = (k == 0 && pw < CPW) ? rx : rw;
+            const uint32_t o = ch[k].off + (uint32_t)w * ch[k].step;
+            const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0));
             r[4 * k] = v.x;
             r[4 * k + 1] = v.y;
             r[4 * k + 2] = v.z;
@@ -317,15 +341,15 @@ __global__ __launch_bounds__(576) void canon_pc_kernel(const float* __restrict__
 #pragma unroll
         for (int k = 0; k < LPL; k++) {
             const int d = ch[k].dst;
-            if (d >= 0) {
-                uint8_t* dst = d == kRawBytes + kXsBytes + kProdBytes ? spare + 16 * pl : raw_of(b) + d;
-                *reinterpret_cast<uint4*>(dst) = make_uint4(r[4 * k], r[4 * k + 1], r[4 * k + 2], r[4 * k + 3]);
-            } else {
+            if (k == 0 && pw < CPW) {
                 float* xd = xs_of(b) + (-1 - d);
                 xd[0] = __uint_as_float(r[4 * k]);
                 xd[XS] = __uint_as_float(r[4 * k + 1]);
                 xd[2 * XS] = __uint_as_float(r[4 * k + 2]);
                 xd[3 * XS] = __uint_as_float(r[4 * k + 3]);
+            } else {
+                uint8_t* dst = d == kRawBytes + kXsBytes + kProdBytes ? spare + 16 * pl : raw_of(b) + d;
+                *reinterpret_cast<uint4*>(dst) = make_uint4(r[4 * k], r[4 * k + 1], r[4 * k + 2], r[4 * k + 3]);
             }
         }
     };
@@ -347,44 +371,47 @@ __global__ __launch_bounds__(576) void canon_pc_kernel(const float* __restrict__
 #pragma unroll
         for (int k2 = 0; k2 < UPL; k2++) {
             const float xa[4] = {xv[k2].x, xv[k2].y, xv[k2].z, xv[k2].w};
-            const int e = un[k2].e0 + w * 256;
-            const bool live = un[k2].live && w < nwin;
             float pr[4];
 #pragma unroll
-            for (int m = 0; m < 4; m++) {
-                const float v = xa[m] * wv[k2][m];
-                pr[m] = (live && e + 8 * m < un[k2].ce) ? v : -0.0f;
+            for (int m = 0; m < 4; m++) pr[m] = xa[m] * wv[k2][m];
+            if (w >= un[k2].full) {  // a partial window or a dead slot
+                const int e = un[k2].e0 + w * 256;
+                const bool live = un[k2].live && w < nwin;
+#pragma unroll
+                for (int m = 0; m < 4; m++) pr[m] = (live && e + 8 * m < un[k2].ce) ? pr[m] : -0.0f;
             }
             *reinterpret_cast<float4*>(prod_of(b) + un[k2].poff) = make_float4(pr[0], pr[1], pr[2], pr[3]);
         }
     };
+    constexpr int NS = Wn::NS;
+    // step i: produce window i, stage window i+1 from its slot, refill that
+    // slot with window i+1+NS
     auto step = [&](int i, typename Wn::Regs& r) __attribute__((always_inline)) {
         const int b = i & 1;
         if (i < nwin) produce(i, b);
         stage(r, b ^ 1);
         __builtin_amdgcn_sched_barrier(0);
-        r = load(i + 5);
+        r = load(i + 1 + NS);
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();
     };
-    // prologue in the loop's load order: windows 1..4 in slots 1,2,3,0
-    typename Wn::Regs r0 = load(0);
-    stage(r0, 0);
+    // prologue in the loop's load order: window 0 staged, windows 1..NS in
+    // slots 1, ..., NS-1, 0
+    typename Wn::Regs rs[NS];
+    rs[0] = load(0);
+    stage(rs[0], 0);
     __builtin_amdgcn_sched_barrier(0);
-    typename Wn::Regs r1 = load(1);
-    __builtin_amdgcn_sched_barrier(0);
-    typename Wn::Regs r2 = load(2);
-    __builtin_amdgcn_sched_barrier(0);
-    typename Wn::Regs r3 = load(3);
-    __builtin_amdgcn_sched_barrier(0);
-    r0 = load(4);
+#pragma unroll
+    for (int s = 1; s < NS; s++) {
+        rs[s] = load(s);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    rs[0] = load(NS);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-    for (int i0 = 0; i0 <= nwin; i0 += 4) {
-        step(i0, r1);      // stages window i0+1 (slot 1), loads i0+5
-        step(i0 + 1, r2);  // stages i0+2, loads i0+6
-        step(i0 + 2, r3);
-        step(i0 + 3, r0);
+    for (int i0 = 0; i0 <= nwin; i0 += NS) {
+#pragma unroll
+        for (int s = 0; s < NS; s++) step(i0 + s, rs[(s + 1) % NS]);
     }
 }
 
