@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void embed_kernel(int type, const uint8_t* __r
     for (int i = threadIdx.x; i < dim; i += blockDim.x) x[i] = embed_elem(type, row, i);
 }
 
-// products in parallel, the sum of squares serially in one lane
+// products in parallel, the sum of squares serially by wave 0
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int n,
                                                        float eps, float* __restrict__ out) {
     extern __shared__ float4 prod4[];
@@ -121,10 +121,10 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
     __shared__ float scale_s;
     for (int i = threadIdx.x; i < n; i += blockDim.x) prod[i] = x[i] * x[i];
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const float sumsq = serial_sum_lds(prod, n);
+    if (threadIdx.x < 64) {
+        const float sumsq = serial_sum_wave(prod, n);
         const float mean = sumsq / (float)n;
-        scale_s = 1.0f / libm::sqrtf(mean + eps);
+        if (threadIdx.x == 0) scale_s = 1.0f / libm::sqrtf(mean + eps);
     }
     __syncthreads();
     const float scale = scale_s;
@@ -260,7 +260,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     mx = block_max(mx, red);
     for (int t = t0; t <= p; t += kAttnThreads) att[t] = libm::expf(att[t] - mx);
     __syncthreads();
-    if (t0 == 0) red[0] = 1.0f / serial_sum_lds(att, p + 1);
+    if (t0 < 64) {
+        const float sum = serial_sum_wave(att, p + 1);
+        if (t0 == 0) red[0] = 1.0f / sum;
+    }
     __syncthreads();
     const float inv = red[0];
     for (int t = t0; t <= p; t += kAttnThreads) att[t] *= inv;
@@ -421,7 +424,7 @@ hipError_t embed(int ggml_type, const uint8_t* table, uint32_t rows, const uint3
 }
 
 hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out, hipStream_t stream) {
-    const size_t lds = (size_t)n * 4;
+    const size_t lds = (size_t)((n + 3) & ~3) * 4;  // the serial sum reads whole float4s
     if (lds > 65536) {
         if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(rms_norm_kernel),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds))

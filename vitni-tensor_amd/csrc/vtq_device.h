@@ -160,97 +160,84 @@ __device__ __forceinline__ float group_tree(float v) {
     return v;
 }
 
-// Serial left-to-right sum of v[0..n) held in LDS (16-byte aligned), by one
-// lane.  Groups of 4G values alternate between two register sets: the loads
-// of group g+1 are issued before the dependent adds of group g (the
-// scheduling barriers keep the compiler from sinking them), so LDS latency
-// hides behind the add chain.
-template <int G>
-__device__ __forceinline__ void add_group(float& s, const float4 (&r)[G]) {
+// Serial left-to-right sum of v[0..n) held in LDS (16-byte aligned).  The
+// chain walks chunks of 128 values; inside a chunk the four groups of 32 are
+// straight-line code with the loads of group g+1 issued before the adds of
+// group g, so LDS latency hides behind the add chain and the compiler's wait
+// counts stay exact (a loop carrying loads across its back edge makes it wait
+// for all of them at the top).  Every calling lane gets the sum; calling it
+// from a whole wave costs no more than from one lane.
+__device__ __forceinline__ void add_group32(float& s, const float4 (&r)[8]) {
 #pragma unroll
-    for (int j = 0; j < G; j++) {
+    for (int j = 0; j < 8; j++) {
         s += r[j].x;
         s += r[j].y;
         s += r[j].z;
         s += r[j].w;
     }
 }
-template <int G = 8>
 __device__ inline float serial_sum_lds(const float* v, int n) {
     const float4* v4 = reinterpret_cast<const float4*>(v);
-    const int ng = n / (4 * G);  // whole groups
     float s = 0.0f;
-    float4 a[G], b[G];
-    if (ng > 0) {
+    const int nc = n >> 7;
+    for (int c = 0; c < nc; c++) {
+        const float4* p = v4 + 32 * c;
+        float4 a[8], b[8];
 #pragma unroll
-        for (int j = 0; j < G; j++) a[j] = v4[j];
+        for (int j = 0; j < 8; j++) a[j] = p[j];
+#pragma unroll
+        for (int j = 0; j < 8; j++) b[j] = p[8 + j];
+        add_group32(s, a);
+#pragma unroll
+        for (int j = 0; j < 8; j++) a[j] = p[16 + j];
+        add_group32(s, b);
+#pragma unroll
+        for (int j = 0; j < 8; j++) b[j] = p[24 + j];
+        add_group32(s, a);
+        add_group32(s, b);
     }
-    int g = 0;
-    for (; g + 1 < ng; g += 2) {
-#pragma unroll
-        for (int j = 0; j < G; j++) b[j] = v4[G * (g + 1) + j];
-        __builtin_amdgcn_sched_barrier(0);
-        add_group(s, a);
-        __builtin_amdgcn_sched_barrier(0);
-        const int gn = g + 2 < ng ? g + 2 : g + 1;  // a valid group; the last refill is unused
-#pragma unroll
-        for (int j = 0; j < G; j++) a[j] = v4[G * gn + j];
-        __builtin_amdgcn_sched_barrier(0);
-        add_group(s, b);
-        __builtin_amdgcn_sched_barrier(0);
-    }
-    if (g < ng) add_group(s, a);
-    for (int i = 4 * G * ng; i < n; i++) s += v[i];
+    for (int i = nc << 7; i < n; i++) s += v[i];
     return s;
 }
 
-// Serial left-to-right sum of 256*nchunks values, fed to the dependent add
-// chain by DPP row broadcasts: one v_add_f32_dpp per element, no LDS read in
-// the chain.  Layout: element 256c + 16i + l sits in LDS at 256c + 16l + i,
-// so lane l (of every 16-lane row) loads its 16 values of chunk c as four
-// float4.  Element order is kept: chunk by chunk, i outer, l inner; IEEE
-// addition is commutative, so bcast(r) + acc equals acc + bcast(r).  Every
-// lane of the calling wave ends with the same sum.
-template <int L>
-__device__ __forceinline__ void add_bcast(float& acc, float r) {
-    asm volatile("v_add_f32_dpp %0, %1, %0 row_newbcast:%2 row_mask:0xf bank_mask:0xf" : "+v"(acc) : "v"(r), "i"(L));
-}
-__device__ __forceinline__ void add_bcast16(float& acc, float r) {
-    add_bcast<0>(acc, r), add_bcast<1>(acc, r), add_bcast<2>(acc, r), add_bcast<3>(acc, r);
-    add_bcast<4>(acc, r), add_bcast<5>(acc, r), add_bcast<6>(acc, r), add_bcast<7>(acc, r);
-    add_bcast<8>(acc, r), add_bcast<9>(acc, r), add_bcast<10>(acc, r), add_bcast<11>(acc, r);
-    add_bcast<12>(acc, r), add_bcast<13>(acc, r), add_bcast<14>(acc, r), add_bcast<15>(acc, r);
-}
-__device__ __forceinline__ void add_chunk(float& acc, const float4 (&r)[4]) {
+// Serial left-to-right sum continued from `run`, over values held in
+// registers, by a whole wave: lane L holds the 32 consecutive values of
+// segment L in r[0..31], segments 0..nl-1 in order.  Every lane runs the
+// same 32 dependent adds starting from the running sum, and readlane takes
+// segment L's result from lane L, so the chain never waits on memory.  The
+// result is the same in every lane.
+__device__ inline float serial_sum_lanes(const float (&r)[32], int nl, float run) {
+    for (int L = 0; L < nl; L++) {
+        float s = run;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        add_bcast16(acc, r[j].x);
-        add_bcast16(acc, r[j].y);
-        add_bcast16(acc, r[j].z);
-        add_bcast16(acc, r[j].w);
+        for (int k = 0; k < 32; k++) s = s + r[k];
+        run = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), L));
     }
+    return run;
 }
-__device__ inline float serial_sum_bcast(const float* v, int nchunks) {
-    const float4* v4 = reinterpret_cast<const float4*>(v) + 4 * (threadIdx.x & 15);
-    float acc = 0.0f;
-    float4 a[4], b[4];
+
+// serial_sum_lanes over v[0..n) in LDS (16-byte aligned, allocated to a
+// multiple of 4 floats), by a whole wave; slots past n read as -0.0, the
+// exact identity of +.
+__device__ inline float serial_sum_wave(const float* v, int n) {
+    const int lane = threadIdx.x & 63;
+    float run = 0.0f;
+    for (int base = 0; base < n; base += 2048) {
+        const int m = n - base < 2048 ? n - base : 2048;
+        float r[32];
 #pragma unroll
-    for (int j = 0; j < 4; j++) a[j] = v4[j];
-    for (int c = 0; c < nchunks; c += 2) {
-        const int c1 = c + 1 < nchunks ? c + 1 : c;
-#pragma unroll
-        for (int j = 0; j < 4; j++) b[j] = v4[64 * c1 + j];
-        __builtin_amdgcn_sched_barrier(0);
-        add_chunk(acc, a);
-        __builtin_amdgcn_sched_barrier(0);
-        const int c2 = c + 2 < nchunks ? c + 2 : c;
-#pragma unroll
-        for (int j = 0; j < 4; j++) a[j] = v4[64 * c2 + j];
-        __builtin_amdgcn_sched_barrier(0);
-        if (c + 1 < nchunks) add_chunk(acc, b);
-        __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < 8; i++) {
+            const int idx = base + 32 * lane + 4 * i;
+            float4 t = make_float4(-0.0f, -0.0f, -0.0f, -0.0f);
+            if (idx < n) t = *reinterpret_cast<const float4*>(v + idx);
+            r[4 * i] = idx < n ? t.x : -0.0f;
+            r[4 * i + 1] = idx + 1 < n ? t.y : -0.0f;
+            r[4 * i + 2] = idx + 2 < n ? t.z : -0.0f;
+            r[4 * i + 3] = idx + 3 < n ? t.w : -0.0f;
+        }
+        run = serial_sum_lanes(r, (m + 31) / 32, run);
     }
-    return acc;
+    return run;
 }
 
 }  // namespace vtq
