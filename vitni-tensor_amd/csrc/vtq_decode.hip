@@ -167,33 +167,31 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float* red = vp + hd;
     float* att = red + kAttnThreads + (4 - (3 * hd) % 4) % 4;  // 16-byte aligned for float4 reads
     float* vt = att + ((a.seq + 3) & ~3);
-    const int p = *a.pos;
     const int t0 = threadIdx.x;
     constexpr bool kFast = HD == 64;
-    const bool fast = kFast && p < kAttnThreads;
-    // q, k, v (+ bias, forward_quantized.rs:390-404), then (fast path) thread
-    // t's cached k row into registers and the cached v rows into LDS: every
-    // load is issued before the first one is waited for
-    float qv = 0.0f, kv = 0.0f, vv = 0.0f;
+    // Every load that does not need the position is issued with it: q, k,
+    // v (+ bias, forward_quantized.rs:390-404), this step's RoPE angles and
+    // (head_dim 64) cached rows 0..kAttnThreads-1, thread t's k row into
+    // registers and all v rows into LDS.  Rows at or past the position hold
+    // older values and are never used; rows past the cache are not read.
+    float qv = 0.0f, kv = 0.0f, vv = 0.0f, rc = 0.0f, rs = 0.0f;
     if (t0 < hd) qv = a.qkv[h * hd + t0], kv = a.qkv[dim + hk * hd + t0], vv = a.qkv[dim + kv_dim + hk * hd + t0];
+    if (t0 < hd / 2) rc = a.cs[2 * t0], rs = a.cs[2 * t0 + 1];
     constexpr int KPT = kFast ? HD / 4 : 1;
     float4 kr[KPT];
     if constexpr (kFast) {
-        // rows >= pos are never used: clamped to row 0, always in bounds
-        const float4* krow = reinterpret_cast<const float4*>(a.kc + (size_t)(t0 < p ? t0 : 0) * kv_dim + hk * hd);
+        const float4* krow = reinterpret_cast<const float4*>(a.kc + (size_t)(t0 < a.seq ? t0 : 0) * kv_dim + hk * hd);
 #pragma unroll
         for (int j = 0; j < KPT; j++) kr[j] = krow[j];
-        if (fast) {
-            // all kAttnThreads * HD/4 float4 of the tile; rows >= pos hold
-            // copies of row 0 and are never read
 #pragma unroll
-            for (int u = 0; u < HD / 4; u++) {
-                const int i = t0 + kAttnThreads * u, t = i / (HD / 4);
-                reinterpret_cast<float4*>(vt)[i] =
-                    reinterpret_cast<const float4*>(a.vc + (size_t)(t < p ? t : 0) * kv_dim + hk * hd)[i % (HD / 4)];
-            }
+        for (int u = 0; u < HD / 4; u++) {
+            const int i = t0 + kAttnThreads * u, t = i / (HD / 4);
+            reinterpret_cast<float4*>(vt)[i] =
+                reinterpret_cast<const float4*>(a.vc + (size_t)(t < a.seq ? t : 0) * kv_dim + hk * hd)[i % (HD / 4)];
         }
     }
+    const int p = *a.pos;
+    const bool fast = kFast && p < kAttnThreads;
     for (int d = t0; d < hd; d += kAttnThreads) {
         float q = d == t0 ? qv : a.qkv[h * hd + d], k = d == t0 ? kv : a.qkv[dim + hk * hd + d],
               v = d == t0 ? vv : a.qkv[dim + kv_dim + hk * hd + d];
@@ -207,7 +205,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     __syncthreads();
     // RoPE with this step's angles (rope_table)
     for (int m = t0; m < hd / 2; m += kAttnThreads) {
-        const float c = a.cs[2 * m], s = a.cs[2 * m + 1];
+        const float c = m == t0 ? rc : a.cs[2 * m], s = m == t0 ? rs : a.cs[2 * m + 1];
         const int i0 = a.neox ? m : 2 * m, i1 = a.neox ? m + hd / 2 : 2 * m + 1;
         const float q0 = qs[i0], q1 = qs[i1], k0 = kp[i0], k1 = kp[i1];
         qs[i0] = q0 * c - q1 * s;
@@ -273,6 +271,33 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     auto accumulate = [&](float& acc, int c0, int nt) {
         if (t0 < hd) {
             int t = 0;
+            // chunks of 32 positions: the loads of group g+1 are issued
+            // before the adds of group g, in straight-line code
+            auto ld = [&](float (&vb)[8], float (&ab)[8], int t1) __attribute__((always_inline)) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    vb[j] = vt[(t1 + j) * hd + t0];
+                    ab[j] = att[c0 + t1 + j];
+                }
+            };
+            auto add = [&](const float (&vb)[8], const float (&ab)[8]) __attribute__((always_inline)) {
+                float pr[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) pr[j] = ab[j] * vb[j];
+#pragma unroll
+                for (int j = 0; j < 8; j++) acc += pr[j];
+            };
+            for (; t + 32 <= nt; t += 32) {
+                float va[8], aa[8], vb[8], ab[8];
+                ld(va, aa, t);
+                ld(vb, ab, t + 8);
+                add(va, aa);
+                ld(va, aa, t + 16);
+                add(vb, ab);
+                ld(vb, ab, t + 24);
+                add(va, aa);
+                add(vb, ab);
+            }
             for (; t + 8 <= nt; t += 8) {
                 float vb[8], ab[8];
 #pragma unroll
