@@ -135,18 +135,16 @@ constexpr int kAttnThreads = 256;
 constexpr int kAttnTile = 256;  // cached v positions per LDS tile at head_dim 64 (64 KiB)
 
 // max in the reference's sense (strict >, NaN never wins), as a tree
+// Largest of the threads' m (none is NaN, so the order of the comparisons
+// is free): within each wave by DPP, then across the waves through red[].
+// red[0..kAttnThreads/64) must not be rewritten before the next barrier.
 __device__ float block_max(float m, float* red) {
-    red[threadIdx.x] = m;
+    m = wave_max_nonneg(m);  // any non-NaN values: the DPP patterns stay inside each row
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
-    for (int s = kAttnThreads / 2; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) {
-            const float o = red[threadIdx.x + s];
-            if (o > red[threadIdx.x]) red[threadIdx.x] = o;
-        }
-        __syncthreads();
-    }
-    const float r = red[0];
-    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < kAttnThreads / 64; w++) r = red[w] > r ? red[w] : r;
     return r;
 }
 
@@ -227,22 +225,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float mx = -__builtin_inff();
     if (fast) {
         if (t0 <= p) {
-            float score = 0.0f;
-            if (t0 < p) {
+            // position p's k is this step's roped k (LDS), the others' the cached row
+            if (t0 == p) {
 #pragma unroll
-                for (int j = 0; j < KPT; j++) {
-                    const float4 q4 = reinterpret_cast<const float4*>(qs)[j];
-                    score += q4.x * kr[j].x;
-                    score += q4.y * kr[j].y;
-                    score += q4.z * kr[j].z;
-                    score += q4.w * kr[j].w;
-                }
-            } else {
-                for (int d = 0; d < hd; d++) score += qs[d] * kp[d];
+                for (int j = 0; j < KPT; j++) kr[j] = reinterpret_cast<const float4*>(kp)[j];
+            }
+            float score = 0.0f;
+#pragma unroll
+            for (int j = 0; j < KPT; j++) {
+                const float4 q4 = reinterpret_cast<const float4*>(qs)[j];
+                score += q4.x * kr[j].x;
+                score += q4.y * kr[j].y;
+                score += q4.z * kr[j].z;
+                score += q4.w * kr[j].w;
             }
             score /= sq;
             att[t0] = score;
-            mx = score;
+            if (score > mx) mx = score;  // a NaN score never becomes the max
         }
     } else {
         for (int t = t0; t <= p; t += kAttnThreads) {
@@ -275,9 +274,15 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
             // before the adds of group g, in straight-line code
             auto ld = [&](float (&vb)[8], float (&ab)[8], int t1) __attribute__((always_inline)) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    vb[j] = vt[(t1 + j) * hd + t0];
-                    ab[j] = att[c0 + t1 + j];
+                for (int j = 0; j < 8; j++) vb[j] = vt[(t1 + j) * hd + t0];
+                if (((c0 + t1) & 3) == 0) {  // the weights as two float4 (wave-uniform test)
+                    const float4 w0 = *reinterpret_cast<const float4*>(att + c0 + t1);
+                    const float4 w1 = *reinterpret_cast<const float4*>(att + c0 + t1 + 4);
+                    ab[0] = w0.x, ab[1] = w0.y, ab[2] = w0.z, ab[3] = w0.w;
+                    ab[4] = w1.x, ab[5] = w1.y, ab[6] = w1.z, ab[7] = w1.w;
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) ab[j] = att[c0 + t1 + j];
                 }
             };
             auto add = [&](const float (&vb)[8], const float (&ab)[8]) __attribute__((always_inline)) {
