@@ -207,10 +207,18 @@ __device__ inline float serial_sum_lds(const float* v, int n) {
 // segment L's result from lane L, so the chain never waits on memory.  The
 // result is the same in every lane.
 __device__ inline float serial_sum_lanes(const float (&r)[32], int nl, float run) {
+    // pin the values in registers: left alone, the compiler re-reads them
+    // from LDS inside the loop and the chain waits on every segment's loads
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+        v[k] = r[k];
+        asm volatile("" : "+v"(v[k]));
+    }
     for (int L = 0; L < nl; L++) {
         float s = run;
 #pragma unroll
-        for (int k = 0; k < 32; k++) s = s + r[k];
+        for (int k = 0; k < 32; k++) s = s + v[k];
         run = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), L));
     }
     return run;
