@@ -17,6 +17,11 @@ SMALL = dict(dim=256, hidden=512, layers=2, heads=4, kv_heads=2, vocab=1000, ctx
              rms_eps=1e-5)
 MEDIUM = dict(dim=512, hidden=1536, layers=4, heads=8, kv_heads=2, vocab=4096, ctx=160, rope_theta=10000.0,
               rms_eps=1e-5)
+# dim 2560: the fused RMSNorm's serial chain over two passes, the second
+# partial; head_dim 128 and positions past 256: attention's general path;
+# hidden 4352: two-window rows for W2
+WIDE = dict(dim=2560, hidden=4352, layers=1, heads=20, kv_heads=4, vocab=512, ctx=300, rope_theta=10000.0,
+            rms_eps=1e-5)
 
 
 def compare(cfg, prompt_len, n_new, regimes=(0, 1), threads=8):
@@ -48,6 +53,10 @@ def test_e2e_medium_odd_lengths():
     # kv heads < heads (GQA), prompt of 1, long generation
     compare(MEDIUM, 1, 40, regimes=(0,))
     compare(MEDIUM, 13, 29, regimes=(1,))
+
+
+def test_e2e_wide_long_context():
+    compare(WIDE, 250, 12, regimes=(0,), threads=16)
 
 
 def test_e2e_errors_mirror_reference():
