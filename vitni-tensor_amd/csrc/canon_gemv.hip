@@ -159,12 +159,13 @@ __global__ __launch_bounds__(256) void canon_gemv_kernel(const float* __restrict
 // 4096-row layer has only 32768 chains (512 waves): summing them is cheap,
 // decoding and multiplying 16.8M elements is not.  So one workgroup = one
 // consumer wave (8 groups of 8 chain lanes, as in canon_gemv_kernel) plus
-// eight producer waves.  The row data is walked in windows of 256 elements:
+// four (eight at eight chunk slots) producer waves.  The row data is walked
+// in windows of 256 elements:
 //  * producers fetch each window's raw weight bytes (whole 16-byte chunks)
 //    and its x values four windows ahead in registers, stage them in LDS
 //    (x transposed chain-major), then decode and form the products
 //    x_i * w_i of the window: 512 units of 4 consecutive chain positions,
-//    one per producer lane;
+//    two (one) per producer lane;
 //  * the consumer adds the previous window's products into its chains in
 //    increasing element order (the reference's sequential lane chains).
 // Products of elements past a chunk's end are written as -0.0, which is the
@@ -183,7 +184,10 @@ struct PcWin {
     static constexpr int NCH = RAWB / 16;             // 16-byte chunks per group window
     static constexpr int XCH = 64 * CPW;              // x chunks per window: the first CPW producer waves
     static constexpr int NLOAD = 8 * NCH + XCH;       // chunks per window: x, then weights
-    static constexpr int NPW = 8;                     // producer waves
+    // producer waves: four (measured faster than eight: a shorter barrier
+    // and less LDS contention per window), eight when the x chunks of
+    // eight chunk slots need them
+    static constexpr int NPW = CPW > 4 ? 8 : 4;
     static constexpr int NP = 64 * NPW;               // producer lanes
     static constexpr int UPL = 512 / NP;              // product units per producer lane
     static constexpr int LPL = (NLOAD + NP - 1) / NP;  // chunk loads per producer lane
@@ -192,6 +196,7 @@ struct PcWin {
     static constexpr int GS = 8 * XS;                 // group stride of the product window
     static constexpr int EPB = Dec::kBlock / 8;       // chain elements per block
     static_assert(WB % 16 == 0, "window byte size");
+    static_assert(512 % NP == 0 && XCH <= NP, "units and x chunks divide over the producer lanes");
 
     // one window's registers as one vector value (stays in registers)
     typedef uint32_t Regs __attribute__((ext_vector_type(4 * LPL)));
@@ -212,7 +217,7 @@ struct PcWin {
 };
 
 template <class Dec, int CPW>
-__global__ __launch_bounds__(576) void canon_pc_kernel(const float* __restrict__ x, const uint8_t* __restrict__ W,
+__global__ __launch_bounds__(64 * (PcWin<Dec, CPW>::NPW + 1)) void canon_pc_kernel(const float* __restrict__ x, const uint8_t* __restrict__ W,
                                                        size_t row_bytes, size_t wbytes, float* __restrict__ y, int n,
                                                        int out_feat, int nchunks, int nwin) {
     using Wn = PcWin<Dec, CPW>;
@@ -425,7 +430,9 @@ static hipError_t launch_pc(const float* x, const uint8_t* w, size_t row_bytes, 
     while (cpw < nchunks) cpw <<= 1;
     const int rows = 8 / cpw;
     dim3 grid((unsigned)((out_feat + rows - 1) / rows), (unsigned)batch, 1);
-#define VTQ_PC(C) hipLaunchKernelGGL((canon_pc_kernel<Dec, C>), grid, dim3(576), 0, stream, x, w, row_bytes, wbytes, y, n, out_feat, nchunks, nwin)
+#define VTQ_PC(C)                                                                                             \
+    hipLaunchKernelGGL((canon_pc_kernel<Dec, C>), grid, dim3(64 * (PcWin<Dec, C>::NPW + 1)), 0, stream, x, w, \
+                       row_bytes, wbytes, y, n, out_feat, nchunks, nwin)
     switch (cpw) {
     case 1: VTQ_PC(1); break;
     case 2: VTQ_PC(2); break;
