@@ -452,37 +452,37 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
     if constexpr (NORM) {
         // rms_norm_slice: x*x per element into LDS past the activation arrays,
         // the sum of squares serially by wave 0 (serial_sum_lanes over passes
-        // of 8 blocks: in pass P, element 32L + k of the pass sits at float
-        // 2048P + 256(k/4) + 4L + k%4, so lane L reads its 32 values as eight
-        // conflict-free float4), then x * scale * w
+        // of 16 blocks: in pass P, element 64L + k of the pass sits at float
+        // 4096P + 256(k/4) + 4L + k%4, so lane L reads its 64 values as
+        // sixteen conflict-free float4), then x * scale * w
         float* prod = reinterpret_cast<float*>(lds + act_lds_end(R));
-        const int npass = (R + 7) / 8;
+        const int npass = (R + 15) / 16;
 #pragma unroll
         for (int j = 0; j < NWIN; j++) {
             const int b = wave + kNW * j;
             const float4 v = xv[j];
-            // elements 256b + 4 lane + c: pass b/8, segment 8(b%8) + lane/8, k = 4(lane%8) + c
+            // elements 256b + 4 lane + c: pass b/16, segment 4(b%16) + lane/16, k = 4(lane%16) + c
             if (b < R)
-                reinterpret_cast<float4*>(prod + 2048 * (b >> 3) + 256 * (lane & 7) + 32 * (b & 7))[lane >> 3] =
+                reinterpret_cast<float4*>(prod + 4096 * (b >> 4) + 256 * (lane & 15) + 16 * (b & 15))[lane >> 4] =
                     make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
         }
         __syncthreads();
         if (wave == 0) {
             float sumsq = 0.0f;
             for (int ps = 0; ps < npass; ps++) {
-                float r[32];
+                float r[64];
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const float4 t = reinterpret_cast<const float4*>(prod + 2048 * ps + 256 * i)[lane];
+                for (int i = 0; i < 16; i++) {
+                    const float4 t = reinterpret_cast<const float4*>(prod + 4096 * ps + 256 * i)[lane];
                     r[4 * i] = t.x, r[4 * i + 1] = t.y, r[4 * i + 2] = t.z, r[4 * i + 3] = t.w;
                 }
-                sumsq = serial_sum_lanes(r, 8 * min(8, R - 8 * ps), sumsq);
+                sumsq = serial_sum_lanes(r, 4 * min(16, R - 16 * ps), sumsq);
             }
             const float mean = sumsq / (float)(R * 256);
-            if (lane == 0) prod[2048 * npass] = 1.0f / libm::sqrtf(mean + args.eps);
+            if (lane == 0) prod[4096 * npass] = 1.0f / libm::sqrtf(mean + args.eps);
         }
         __syncthreads();
-        const float scale = prod[2048 * npass];
+        const float scale = prod[4096 * npass];
 #pragma unroll
         for (int j = 0; j < NWIN; j++) {
             const float4 v = xv[j], w = nw[j];
@@ -647,7 +647,7 @@ static hipError_t launch(K kern, int wgs, int batch, int R, hipStream_t stream, 
     return launch_lds(kern, wgs, batch, act_lds_bytes(R), stream, a...);
 }
 // the normalising prologue keeps the products (passes of 2048 floats) and the scale past the activation arrays
-static size_t norm_lds_bytes(int R) { return act_lds_bytes(R) + (size_t)(R + 7) / 8 * 8192 + 16; }
+static size_t norm_lds_bytes(int R) { return act_lds_bytes(R) + (size_t)(R + 15) / 16 * 16384 + 16; }
 
 // one 16-wave workgroup per CU; more if a wave would own over 64 rows
 static int rows_grid(int out_feat, int num_cus) {

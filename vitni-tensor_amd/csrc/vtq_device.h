@@ -201,24 +201,25 @@ __device__ inline float serial_sum_lds(const float* v, int n) {
 }
 
 // Serial left-to-right sum continued from `run`, over values held in
-// registers, by a whole wave: lane L holds the 32 consecutive values of
-// segment L in r[0..31], segments 0..nl-1 in order.  Every lane runs the
-// same 32 dependent adds starting from the running sum, and readlane takes
+// registers, by a whole wave: lane L holds the V consecutive values of
+// segment L in r[0..V), segments 0..nl-1 in order.  Every lane runs the
+// same V dependent adds starting from the running sum, and readlane takes
 // segment L's result from lane L, so the chain never waits on memory.  The
 // result is the same in every lane.
-__device__ inline float serial_sum_lanes(const float (&r)[32], int nl, float run) {
+template <int V>
+__device__ inline float serial_sum_lanes(const float (&r)[V], int nl, float run) {
     // pin the values in registers: left alone, the compiler re-reads them
     // from LDS inside the loop and the chain waits on every segment's loads
-    float v[32];
+    float v[V];
 #pragma unroll
-    for (int k = 0; k < 32; k++) {
+    for (int k = 0; k < V; k++) {
         v[k] = r[k];
         asm volatile("" : "+v"(v[k]));
     }
     for (int L = 0; L < nl; L++) {
         float s = run;
 #pragma unroll
-        for (int k = 0; k < 32; k++) s = s + v[k];
+        for (int k = 0; k < V; k++) s = s + v[k];
         run = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), L));
     }
     return run;
