@@ -373,9 +373,23 @@ struct Q6K {
 // ------------------------------------------------------------ rows kernel
 
 // Row j of wave gw is gw + j*tw (tw = waves in the grid); lane j keeps that
-// row's result and the wave stores its rows once at the end.  PRE of the D
-// ring slots are loaded before the activation is quantized (their data then
-// shares the memory system with the activation reads), the rest after.
+// row's result and the wave stores its rows once at the end.  Waves are
+// numbered in groups of four: wave w of workgroup b is
+// gw = 4*(b + G*(w/4)) + w%4 (G workgroups), so each workgroup reads four
+// bands of four consecutive rows, and consecutive 4-row bands fall on
+// consecutive workgroups (hence on different XCDs).  Measured faster than
+// 16 consecutive rows per workgroup.
+//
+// Weight loads issued before the activation is quantized share the memory
+// system with the activation reads and delay them (the activation is needed
+// by every workgroup before any weight can be used), so how much is issued
+// early is tuned per shape:
+//   PRE   ring slots (whole rows) loaded before the activation reads return;
+//   PREW  (PRE = 0 only) windows of row 0 loaded before the activation reads
+//         return, the rest of the row after the workgroup's quantization;
+//   POSTX the remaining D - PRE slots are issued as soon as this wave's own
+//         activation reads have returned (before quantizing), instead of
+//         after the workgroup barrier.
 //
 // The output rows are the concatenation of up to three weight matrices that
 // share the activation (RowsArgs); EPI selects what is stored:
@@ -384,7 +398,7 @@ struct Q6K {
 //   kEpiSwiGLU      two matrices of equal rows; y[i] = silu(g) * u with
 //                   g = W0 row i . x, u = W1 row i . x and silu(g) =
 //                   g / (1 + expf(-g))  (forward_quantized.rs SwiGLU)
-template <class Fmt, int NWIN, int D, int PRE, int EPI, bool MULTI, bool NORM>
+template <class Fmt, int NWIN, int D, int PRE, int PREW, bool POSTX, int EPI, bool MULTI, bool NORM>
 __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __restrict__ x, RowsArgs args,
                                                                float* __restrict__ y, int R) {
     constexpr int NM = EPI == kEpiSwiGLU ? 2 : 1;  // matrices read per output row
@@ -397,7 +411,9 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
     const float* xb = x + (size_t)blockIdx.y * R * 256;
     float* yb = y + (size_t)blockIdx.y * out_feat;
     const uint32_t row_bytes = (uint32_t)R * Fmt::kBytes;
-    const int tw = gridDim.x * kNW, gw = blockIdx.x * kNW + wave;
+    static_assert(PREW == 0 || (PRE == 0 && PREW < NWIN && !POSTX), "PREW splits row 0 of a PRE = 0 ring");
+    const int tw = gridDim.x * kNW;
+    const int gw = 4 * ((int)blockIdx.x + (int)gridDim.x * (wave >> 2)) + (wave & 3);
     const int nrows = gw < out_feat ? (out_feat - 1 - gw) / tw + 1 : 0;  // <= 64 (launcher)
 
     // R <= 16 * NWIN: each wave holds at most NWIN activation blocks
@@ -419,7 +435,8 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
     };
     const int c1 = args.rows[0], c2 = args.rows[0] + args.rows[1];
     typename Fmt::Regs buf[D][NM][NWIN];
-    auto load_row = [&](typename Fmt::Regs (&rb)[NM][NWIN], int j) {
+    // windows [w0, w1) of the j-th row of this wave
+    auto load_row = [&](typename Fmt::Regs (&rb)[NM][NWIN], int j, int w0 = 0, int w1 = NWIN) {
         const int r = gw + j * tw;
         if constexpr (EPI == kEpiSwiGLU) {
             const uint32_t ro = j < nrows ? (uint32_t)r * row_bytes : kOutOfRange;
@@ -427,13 +444,15 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
             for (int m = 0; m < 2; m++) {
                 const __amdgpu_buffer_rsrc_t rs = rsrc(args.w[m], args.rows[m]);
 #pragma unroll
-                for (int w = 0; w < NWIN; w++) Fmt::bload(rb[m][w], rs, ro + boff[w], k);
+                for (int w = 0; w < NWIN; w++)
+                    if (w >= w0 && w < w1) Fmt::bload(rb[m][w], rs, ro + boff[w], k);
             }
         } else if constexpr (!MULTI) {
             const uint32_t ro = j < nrows ? (uint32_t)r * row_bytes : kOutOfRange;
             const __amdgpu_buffer_rsrc_t rs = rsrc(args.w[0], args.rows[0]);
 #pragma unroll
-            for (int w = 0; w < NWIN; w++) Fmt::bload(rb[0][w], rs, ro + boff[w], k);
+            for (int w = 0; w < NWIN; w++)
+                    if (w >= w0 && w < w1) Fmt::bload(rb[0][w], rs, ro + boff[w], k);
         } else {
             // segment of row r (wave-uniform): the matrix and the row inside it
             const int sg = (r >= c1) + (r >= c2);
@@ -442,13 +461,25 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
             const __amdgpu_buffer_rsrc_t rsel = rsrc(sg == 0 ? args.w[0] : sg == 1 ? args.w[1] : args.w[2],
                                                      sg == 0 ? args.rows[0] : sg == 1 ? args.rows[1] : args.rows[2]);
 #pragma unroll
-            for (int w = 0; w < NWIN; w++) Fmt::bload(rb[0][w], rsel, ro + boff[w], k);
+            for (int w = 0; w < NWIN; w++)
+                    if (w >= w0 && w < w1) Fmt::bload(rb[0][w], rsel, ro + boff[w], k);
         }
     };
 #pragma unroll
     for (int i = 0; i < PRE; i++) load_row(buf[i], i);
+    if constexpr (PREW > 0) load_row(buf[0], 0, 0, PREW);
     // keep the x-dependent math (and its wait on the x loads) below the weight loads just issued
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (POSTX) {
+        // an empty use of every activation register makes the compiler wait
+        // for the activation loads here (vmcnt counts the loads issued after
+        // them, so the wait is exact); then the rest of the ring is issued
+#pragma unroll
+        for (int j = 0; j < NWIN; j++) asm volatile("" ::"v"(xv[j].x), "v"(xv[j].y), "v"(xv[j].z), "v"(xv[j].w));
+#pragma unroll
+        for (int i = PRE; i < D; i++) load_row(buf[i], i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     if constexpr (NORM) {
         // rms_norm_slice: x*x per element into LDS past the activation arrays,
         // the sum of squares serially by wave 0 (serial_sum_lanes over passes
@@ -496,8 +527,11 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
 #pragma unroll
     for (int w = 0; w < NWIN; w++) Fmt::load_x(xr[w], act, 16 * w + g < R ? 16 * w + g : R - 1, k);
     const typename Fmt::Lane lc = Fmt::lane_consts(k);
+    if constexpr (PREW > 0) load_row(buf[0], 0, PREW, NWIN);
+    if constexpr (!POSTX) {
 #pragma unroll
-    for (int i = PRE; i < D; i++) load_row(buf[i], i);
+        for (int i = PRE + (PREW > 0); i < D; i++) load_row(buf[i], i);
+    }
 
     float yacc = 0.0f;
     for (int j0 = 0; j0 < nrows; j0 += D) {
@@ -655,25 +689,30 @@ static int rows_grid(int out_feat, int num_cus) {
     return num_cus < need ? need : num_cus;
 }
 
-// Ring depth D and pre-quantization loads PRE of the rows kernel: one-window
-// rows keep two rows in flight, one of them issued before the activation
-// pass; longer rows keep a single row in flight, issued after it (Q4_K
-// two-window rows still fit two).  Deeper rings spill registers.
+// Ring depth D and early loads of the rows kernel (measured on the config-2
+// shapes): one-window rows keep two rows in flight, one issued before the
+// activation reads and one as soon as they return; three-window rows keep a
+// single row in flight whose first window is issued before the activation
+// reads.  Two-window rows keep two (Q4_K) or one (Q6_K, SwiGLU) rows in
+// flight.  Deeper rings spill registers.
 template <class Fmt, int EPI, bool MULTI, bool NORM = false>
 static hipError_t launch_rows(int nwin, int wgs, int batch, int R, const float* x, const RowsArgs& a, float* y,
                               hipStream_t stream) {
     const size_t lds = NORM ? norm_lds_bytes(R) : act_lds_bytes(R);
     if (nwin == 1)
-        return launch_lds(kquant_rows_kernel<Fmt, 1, 2, 1, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a, y, R);
+        return launch_lds(kquant_rows_kernel<Fmt, 1, 2, 1, 0, true, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a,
+                          y, R);
     if constexpr (MULTI && Fmt::kRowsMaxWindows == 2) {
         return hipErrorInvalidValue;  // Q6_K segment selection at two windows would spill registers
     } else if constexpr (Fmt::kRowsMaxWindows == 2 || EPI == kEpiSwiGLU) {
-        return launch_lds(kquant_rows_kernel<Fmt, 2, 1, 0, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a, y, R);
+        return launch_lds(kquant_rows_kernel<Fmt, 2, 1, 0, 0, false, EPI, MULTI, NORM>, wgs, batch, lds, stream, x,
+                          a, y, R);
     } else {
         if (nwin == 2)
-            return launch_lds(kquant_rows_kernel<Fmt, 2, 2, 1, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a, y,
-                              R);
-        return launch_lds(kquant_rows_kernel<Fmt, 3, 1, 0, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a, y, R);
+            return launch_lds(kquant_rows_kernel<Fmt, 2, 2, 1, 0, false, EPI, MULTI, NORM>, wgs, batch, lds, stream,
+                              x, a, y, R);
+        return launch_lds(kquant_rows_kernel<Fmt, 3, 1, 0, 1, false, EPI, MULTI, NORM>, wgs, batch, lds, stream, x,
+                          a, y, R);
     }
 }
 
