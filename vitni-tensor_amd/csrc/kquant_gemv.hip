@@ -390,6 +390,9 @@ struct Q6K {
 //   POSTX the remaining D - PRE slots are issued as soon as this wave's own
 //         activation reads have returned (before quantizing), instead of
 //         after the workgroup barrier.
+// With PREW, a workgroup barrier right after the activation loads are issued
+// makes every wave's activation requests precede every weight request of the
+// workgroup in the CU's memory pipeline.
 //
 // The output rows are the concatenation of up to three weight matrices that
 // share the activation (RowsArgs); EPI selects what is stored:
@@ -420,6 +423,7 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
     float4 xv[NWIN], nw[NWIN];
     load_act(xv, xb, R, wave);
     if constexpr (NORM) load_act(nw, args.norm_w, R, wave);
+    if constexpr (PREW > 0) __builtin_amdgcn_s_barrier();
 
     uint32_t boff[NWIN];
     bool valid[NWIN];
