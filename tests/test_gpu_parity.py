@@ -74,8 +74,11 @@ def check(ctx, ggml_type, regime, x, w, batch, in_f, out_f):
 
 # ------------------------------------------------------------ k-quant integer
 
+# rows of at most 8 super-blocks (in_feat <= 2048) go two to a wave step: odd row
+# counts leave the last pair half empty; batch > 1 runs one grid slice per row
 KQ_SHAPES = [(1, 256, 1), (1, 256, 3), (1, 512, 7), (1, 4096, 64), (1, 11008, 17), (3, 4096, 300),
-             (1, 2048, 2048), (1, 2048, 256), (1, 5632, 2048), (2, 4096 * 4 + 256, 33), (1, 32768, 9)]
+             (1, 2048, 2048), (1, 2048, 256), (1, 5632, 2048), (2, 4096 * 4 + 256, 33), (1, 32768, 9),
+             (2, 2048, 7), (3, 1792, 4099)]
 
 
 @pytest.mark.parametrize("batch,in_f,out_f", KQ_SHAPES)

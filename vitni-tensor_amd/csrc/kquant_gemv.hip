@@ -156,6 +156,16 @@ __device__ __forceinline__ float window16_tree(float v) {
     v = dpp_add_f<0x143, 0x8>(v);  // row_bcast:31 into row 3
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
+// The same for two rows of at most 8 block slots each, row h in lanes
+// 32h..32h+31: strides 1, 2 and 4 of window16_tree; the sums end in lanes 31
+// (row 0) and 63 (row 1).
+__device__ __forceinline__ float2 window8x2_tree(float v) {
+    v = dpp_add_f<0x114, 0xF>(v);  // row_shr:4
+    v = dpp_add_f<0x118, 0xF>(v);  // row_shr:8
+    v = dpp_add_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    return make_float2(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31)),
+                       __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)));
+}
 
 // ------------------------------------------------------- raw buffer loads
 
@@ -401,7 +411,11 @@ struct Q6K {
 //   kEpiSwiGLU      two matrices of equal rows; y[i] = silu(g) * u with
 //                   g = W0 row i . x, u = W1 row i . x and silu(g) =
 //                   g / (1 + expf(-g))  (forward_quantized.rs SwiGLU)
-template <class Fmt, int NWIN, int D, int PRE, int PREW, bool POSTX, int EPI, bool MULTI, bool NORM>
+//
+// HALF (rows of at most 8 super-blocks): a wave step takes a pair of rows,
+// lanes 32h + 4g + k on row 2p + h, so no lane holds a padding slot; the
+// unit dealt to waves is the pair, and lane j stores pair j's two results.
+template <class Fmt, int NWIN, int D, int PRE, int PREW, bool POSTX, int EPI, bool MULTI, bool NORM, bool HALF = false>
 __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __restrict__ x, RowsArgs args,
                                                                float* __restrict__ y, int R) {
     constexpr int NM = EPI == kEpiSwiGLU ? 2 : 1;  // matrices read per output row
@@ -409,7 +423,9 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
     const ActLds act = act_lds_layout(lds, R);
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
-    const int g = lane >> 2, k = lane & 3;
+    static_assert(!HALF || NWIN == 1, "HALF pairs rows of one window");
+    constexpr int RPS = HALF ? 2 : 1;  // rows per wave step
+    const int g = HALF ? ((lane >> 2) & 7) : (lane >> 2), k = lane & 3, hh = HALF ? lane >> 5 : 0;
     const int out_feat = EPI == kEpiSwiGLU ? args.rows[0] : args.rows[0] + args.rows[1] + args.rows[2];
     const float* xb = x + (size_t)blockIdx.y * R * 256;
     float* yb = y + (size_t)blockIdx.y * out_feat;
@@ -417,7 +433,8 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
     static_assert(PREW == 0 || (PRE == 0 && PREW < NWIN && !POSTX), "PREW splits row 0 of a PRE = 0 ring");
     const int tw = gridDim.x * kNW;
     const int gw = 4 * ((int)blockIdx.x + (int)gridDim.x * (wave >> 2)) + (wave & 3);
-    const int nrows = gw < out_feat ? (out_feat - 1 - gw) / tw + 1 : 0;  // <= 64 (launcher)
+    const int units = (out_feat + RPS - 1) / RPS;
+    const int nrows = gw < units ? (units - 1 - gw) / tw + 1 : 0;  // steps of this wave, <= 64 (launcher)
 
     // R <= 16 * NWIN: each wave holds at most NWIN activation blocks
     float4 xv[NWIN], nw[NWIN];
@@ -441,9 +458,10 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
     typename Fmt::Regs buf[D][NM][NWIN];
     // windows [w0, w1) of the j-th row of this wave
     auto load_row = [&](typename Fmt::Regs (&rb)[NM][NWIN], int j, int w0 = 0, int w1 = NWIN) {
-        const int r = gw + j * tw;
+        const int rp = RPS * (gw + j * tw), r = rp + hh;  // rp: the step's first row (wave-uniform)
+        const bool in = j < nrows && r < out_feat;
         if constexpr (EPI == kEpiSwiGLU) {
-            const uint32_t ro = j < nrows ? (uint32_t)r * row_bytes : kOutOfRange;
+            const uint32_t ro = in ? (uint32_t)r * row_bytes : kOutOfRange;
 #pragma unroll
             for (int m = 0; m < 2; m++) {
                 const __amdgpu_buffer_rsrc_t rs = rsrc(args.w[m], args.rows[m]);
@@ -452,16 +470,18 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
                     if (w >= w0 && w < w1) Fmt::bload(rb[m][w], rs, ro + boff[w], k);
             }
         } else if constexpr (!MULTI) {
-            const uint32_t ro = j < nrows ? (uint32_t)r * row_bytes : kOutOfRange;
+            const uint32_t ro = in ? (uint32_t)r * row_bytes : kOutOfRange;
             const __amdgpu_buffer_rsrc_t rs = rsrc(args.w[0], args.rows[0]);
 #pragma unroll
             for (int w = 0; w < NWIN; w++)
                     if (w >= w0 && w < w1) Fmt::bload(rb[0][w], rs, ro + boff[w], k);
         } else {
-            // segment of row r (wave-uniform): the matrix and the row inside it
-            const int sg = (r >= c1) + (r >= c2);
+            // segment of the step (wave-uniform; with HALF the launcher keeps
+            // segment boundaries even, so both rows of a pair share it): the
+            // matrix and the row inside it
+            const int sg = (rp >= c1) + (rp >= c2);
             const int lr = r - (sg == 0 ? 0 : sg == 1 ? c1 : c2);
-            const uint32_t ro = j < nrows ? (uint32_t)lr * row_bytes : kOutOfRange;
+            const uint32_t ro = in ? (uint32_t)lr * row_bytes : kOutOfRange;
             const __amdgpu_buffer_rsrc_t rsel = rsrc(sg == 0 ? args.w[0] : sg == 1 ? args.w[1] : args.w[2],
                                                      sg == 0 ? args.rows[0] : sg == 1 ? args.rows[1] : args.rows[2]);
 #pragma unroll
@@ -537,33 +557,52 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
         for (int i = PRE + (PREW > 0); i < D; i++) load_row(buf[i], i);
     }
 
-    float yacc = 0.0f;
+    float yacc = 0.0f, yacc1 = 0.0f;  // results of the step's row (HALF: and of its second row)
     for (int j0 = 0; j0 < nrows; j0 += D) {
 #pragma unroll
         for (int i = 0; i < D; i++) {
             if (j0 + i < nrows) {
-                float rv[NM];
+                float rv[NM], rv1[NM];
 #pragma unroll
                 for (int m = 0; m < NM; m++) {
-                    float wv[NWIN];
+                    if constexpr (HALF) {
+                        const float2 s2 = window8x2_tree(Fmt::part(buf[i][m][0], xr[0], lc, valid[0]));
+                        rv[m] = s2.x;
+                        rv1[m] = s2.y;
+                    } else {
+                        float wv[NWIN];
 #pragma unroll
-                    for (int w = 0; w < NWIN; w++)
-                        wv[w] = window16_tree(Fmt::part(buf[i][m][w], xr[w], lc, valid[w]));
-                    rv[m] = windows_tree<NWIN>(wv);
+                        for (int w = 0; w < NWIN; w++)
+                            wv[w] = window16_tree(Fmt::part(buf[i][m][w], xr[w], lc, valid[w]));
+                        rv[m] = windows_tree<NWIN>(wv);
+                    }
                 }
-                float v = rv[0];
-                if constexpr (EPI == kEpiSwiGLU) v = (rv[0] / (1.0f + libm::expf(-rv[0]))) * rv[1];
+                float v = rv[0], v1 = HALF ? rv1[0] : 0.0f;
+                if constexpr (EPI == kEpiSwiGLU) {
+                    v = (rv[0] / (1.0f + libm::expf(-rv[0]))) * rv[1];
+                    if constexpr (HALF) v1 = (rv1[0] / (1.0f + libm::expf(-rv1[0]))) * rv1[1];
+                }
                 yacc = (lane == j0 + i) ? v : yacc;
+                if constexpr (HALF) yacc1 = (lane == j0 + i) ? v1 : yacc1;
             }
             load_row(buf[i], j0 + i + D);
         }
     }
     if (lane < nrows) {
-        float* yp = yb + gw + lane * tw;
+        const int r0 = RPS * (gw + lane * tw);
+        float* yp = yb + r0;
         if constexpr (EPI == kEpiAccumulate)
-            *yp = *yp + yacc;
+            yp[0] = yp[0] + yacc;
         else
-            *yp = yacc;
+            yp[0] = yacc;
+        if constexpr (HALF) {
+            if (r0 + 1 < out_feat) {
+                if constexpr (EPI == kEpiAccumulate)
+                    yp[1] = yp[1] + yacc1;
+                else
+                    yp[1] = yacc1;
+            }
+        }
     }
 }
 
@@ -703,6 +742,11 @@ template <class Fmt, int EPI, bool MULTI, bool NORM = false>
 static hipError_t launch_rows(int nwin, int wgs, int batch, int R, const float* x, const RowsArgs& a, float* y,
                               hipStream_t stream) {
     const size_t lds = NORM ? norm_lds_bytes(R) : act_lds_bytes(R);
+    // rows of at most 8 super-blocks go two to a wave step (segment
+    // boundaries of a multi-matrix launch must then be even)
+    if (nwin == 1 && R <= 8 && (!MULTI || (a.rows[0] % 2 == 0 && a.rows[1] % 2 == 0)))
+        return launch_lds(kquant_rows_kernel<Fmt, 1, 2, 1, 0, true, EPI, MULTI, NORM, true>, wgs, batch, lds, stream, x,
+                          a, y, R);
     if (nwin == 1)
         return launch_lds(kquant_rows_kernel<Fmt, 1, 2, 1, 0, true, EPI, MULTI, NORM>, wgs, batch, lds, stream, x, a,
                           y, R);
