@@ -579,8 +579,16 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
                 }
                 float v = rv[0], v1 = HALF ? rv1[0] : 0.0f;
                 if constexpr (EPI == kEpiSwiGLU) {
-                    v = (rv[0] / (1.0f + libm::expf(-rv[0]))) * rv[1];
-                    if constexpr (HALF) v1 = (rv1[0] / (1.0f + libm::expf(-rv1[0]))) * rv1[1];
+                    if constexpr (HALF) {
+                        // lanes 0..31 evaluate the first row's silu(g) * u, lanes
+                        // 32..63 the second row's, in one pass
+                        const float gs = hh ? rv1[0] : rv[0], us = hh ? rv1[1] : rv[1];
+                        const float vs = (gs / (1.0f + libm::expf(-gs))) * us;
+                        v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vs), 0));
+                        v1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(vs), 32));
+                    } else {
+                        v = (rv[0] / (1.0f + libm::expf(-rv[0]))) * rv[1];
+                    }
                 }
                 yacc = (lane == j0 + i) ? v : yacc;
                 if constexpr (HALF) yacc1 = (lane == j0 + i) ? v1 : yacc1;
