@@ -151,8 +151,11 @@ __device__ float block_max(float m, float* red) {
 // One workgroup per query head h.  Shared: q (roped), this step's k (roped)
 // and v of h's KV head, then the attention weights of positions 0..pos.
 // HD > 0: the head dimension as a compile-time constant; with HD == 64 and
-// pos < kAttnThreads every global load of the kernel (q, k, v, the rope
-// angles, thread t's cached k row, the cached v rows) is issued at once.
+// pos < kAttnThreads the position is read first, every load that does not
+// need it (q, k, v, the rope angles, thread t's cached k row) is issued
+// with it, and the cached v rows 0..pos are issued as soon as it returns
+// and stored to LDS only after the softmax, so they arrive behind the
+// scores.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     extern __shared__ float4 sh4[];
@@ -167,29 +170,41 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float* vt = att + ((a.seq + 3) & ~3);
     const int t0 = threadIdx.x;
     constexpr bool kFast = HD == 64;
-    // Every load that does not need the position is issued with it: q, k,
-    // v (+ bias, forward_quantized.rs:390-404), this step's RoPE angles and
-    // (head_dim 64) cached rows 0..kAttnThreads-1, thread t's k row into
-    // registers and all v rows into LDS.  Rows at or past the position hold
-    // older values and are never used; rows past the cache are not read.
+    // The position first, then every load that does not need it: q, k, v
+    // (+ bias, forward_quantized.rs:390-404), this step's RoPE angles and
+    // (head_dim 64) thread t's cached k row t into registers.  Rows at or
+    // past the position hold older values and are never used; rows past the
+    // cache are not read.
+    const int p = *a.pos;
     float qv = 0.0f, kv = 0.0f, vv = 0.0f, rc = 0.0f, rs = 0.0f;
     if (t0 < hd) qv = a.qkv[h * hd + t0], kv = a.qkv[dim + hk * hd + t0], vv = a.qkv[dim + kv_dim + hk * hd + t0];
     if (t0 < hd / 2) rc = a.cs[2 * t0], rs = a.cs[2 * t0 + 1];
     constexpr int KPT = kFast ? HD / 4 : 1;
-    float4 kr[KPT];
+    float4 kr[KPT], vr[KPT];
+    const bool fast = kFast && p < kAttnThreads;
     if constexpr (kFast) {
-        const float4* krow = reinterpret_cast<const float4*>(a.kc + (size_t)(t0 < a.seq ? t0 : 0) * kv_dim + hk * hd);
+        // cached rows 0..pos-1 (fast path): thread t's k row t, and float4
+        // i = t0 + kAttnThreads*u of the head's v rows, as raw buffer loads
+        // whose unneeded slots get an out-of-range offset (zeros, no memory
+        // traffic), so every load is unconditional and the wait counts stay
+        // exact
+        const size_t cbytes = (size_t)a.seq * kv_dim * 4;
+        const int nrec = (int)(cbytes < 0x7FFFFFF0u ? cbytes : 0x7FFFFFF0u);
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kc, (short)0, nrec, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vc, (short)0, nrec, 0x00020000);
+        const uint32_t koff = fast && t0 < p ? (uint32_t)(((size_t)t0 * kv_dim + hk * hd) * 4) : 0x80000000u;
 #pragma unroll
-        for (int j = 0; j < KPT; j++) kr[j] = krow[j];
+        for (int j = 0; j < KPT; j++)
+            kr[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 16 * j, 0, 0));
+        const int nv = fast ? p * (HD / 4) : 0;
 #pragma unroll
-        for (int u = 0; u < HD / 4; u++) {
+        for (int u = 0; u < KPT; u++) {
             const int i = t0 + kAttnThreads * u, t = i / (HD / 4);
-            reinterpret_cast<float4*>(vt)[i] =
-                reinterpret_cast<const float4*>(a.vc + (size_t)(t < a.seq ? t : 0) * kv_dim + hk * hd)[i % (HD / 4)];
+            const uint32_t off = i < nv ? (uint32_t)(((size_t)t * kv_dim + hk * hd) * 4 + 16 * (i % (HD / 4)))
+                                        : 0x80000000u;
+            vr[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
         }
     }
-    const int p = *a.pos;
-    const bool fast = kFast && p < kAttnThreads;
     for (int d = t0; d < hd; d += kAttnThreads) {
         float q = d == t0 ? qv : a.qkv[h * hd + d], k = d == t0 ? kv : a.qkv[dim + hk * hd + d],
               v = d == t0 ? vv : a.qkv[dim + kv_dim + hk * hd + d];
@@ -318,6 +333,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     };
     float acc = 0.0f;
     if (fast) {
+#pragma unroll
+        for (int u = 0; u < KPT; u++) reinterpret_cast<float4*>(vt)[t0 + kAttnThreads * u] = vr[u];
         __syncthreads();
         accumulate(acc, 0, p);
     } else {
