@@ -745,7 +745,8 @@ static int rows_grid(int out_feat, int num_cus) {
 // activation reads and one as soon as they return; three-window rows keep a
 // single row in flight whose first window is issued before the activation
 // reads.  Two-window rows keep two (Q4_K) or one (Q6_K, SwiGLU) rows in
-// flight.  Deeper rings spill registers.
+// flight; at most one Q4_K row per wave takes the three-window scheme.
+// Deeper rings spill registers.
 template <class Fmt, int EPI, bool MULTI, bool NORM = false>
 static hipError_t launch_rows(int nwin, int wgs, int batch, int R, const float* x, const RowsArgs& a, float* y,
                               hipStream_t stream) {
@@ -764,9 +765,16 @@ static hipError_t launch_rows(int nwin, int wgs, int batch, int R, const float* 
         return launch_lds(kquant_rows_kernel<Fmt, 2, 1, 0, 0, false, EPI, MULTI, NORM>, wgs, batch, lds, stream, x,
                           a, y, R);
     } else {
-        if (nwin == 2)
+        if (nwin == 2) {
+            // at most one row per wave (2048 x 5632 W2 of the decode step:
+            // 5.32 -> 4.62 us): a single ring slot whose first window is
+            // issued before the activation loads return
+            if (a.rows[0] + a.rows[1] + a.rows[2] <= wgs * kNW)
+                return launch_lds(kquant_rows_kernel<Fmt, 2, 1, 0, 1, false, EPI, MULTI, NORM>, wgs, batch, lds,
+                                  stream, x, a, y, R);
             return launch_lds(kquant_rows_kernel<Fmt, 2, 2, 1, 0, false, EPI, MULTI, NORM>, wgs, batch, lds, stream,
                               x, a, y, R);
+        }
         return launch_lds(kquant_rows_kernel<Fmt, 3, 1, 0, 1, false, EPI, MULTI, NORM>, wgs, batch, lds, stream, x,
                           a, y, R);
     }
