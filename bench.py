@@ -76,6 +76,61 @@ def calibrate_copy(mib):
                       "copies": 20}), flush=True)
 
 
+def measured_ceilings(dw, step_bytes_per_launch, gemm_shape, steps):
+    """Reference points measured on this GPU in the same run (BASELINE.md asks
+    for a measured stream peak and MFMA peak beside the published ones):
+    * stream: a plain device-to-device copy (torch copy_) of each rotated
+      weight copy into one destination, read + write bytes counted: the HBM
+      rate of the simplest library kernel on buffers of this size, launch
+      floor included;
+    * mfma: hipBLASLt's int8 GEMM (torch._int_mm) at the prefill shape, the
+      int8 rate a vendor GEMM reaches (it computes a plain int32 product, not
+      the reference's Q4_K arithmetic)."""
+    import torch
+
+    out = {}
+    flat = [w for copies in dw for w in copies]
+    dst = torch.empty_like(flat[0])
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = max(steps, 20)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for k in range(n):
+            dst[: flat[k % len(flat)].numel()].copy_(flat[k % len(flat)])
+    g.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / n * 1e3
+    nbytes = 2 * statistics.mean(w.numel() for w in flat)
+    out["stream"] = {"kernel": "device-to-device copy of the rotated weight copies (graph-replayed), read + write",
+                     "bytes_per_launch": int(nbytes), "us_per_launch": round(us, 3),
+                     "gb_s": round(nbytes / us / 1e3, 1), "frac_of_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+    if gemm_shape is not None and hasattr(torch, "_int_mm"):
+        m, k_, nn = gemm_shape
+        a = torch.randint(-127, 128, (m, k_), dtype=torch.int8, device=flat[0].device)
+        b = torch.randint(-127, 128, (k_, nn), dtype=torch.int8, device=flat[0].device)
+        try:
+            for _ in range(3):
+                torch._int_mm(a, b)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(20):
+                torch._int_mm(a, b)
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / 20 * 1e3
+            tops = 2.0 * m * k_ * nn / us / 1e6
+            out["mfma"] = {"kernel": f"torch._int_mm int8 {m}x{k_} @ {k_}x{nn} -> int32 (hipBLASLt)",
+                           "us_per_launch": round(us, 3), "tops": round(tops, 1),
+                           "frac_of_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
+        except RuntimeError as e:  # not every build ships the int8 GEMM
+            out["mfma"] = {"unavailable": str(e)[:120]}
+    return out
+
+
 def cpu_baseline(cfgs, inputs, seconds):
     """The reference path restated in C (oracle), row-parallel on this host's cores."""
     import oracle
@@ -308,6 +363,8 @@ def main():
             "bytes_per_launch": [c.algorithmic_bytes() for c in cfgs],
         },
     }
+    out["measured_ceilings"] = measured_ceilings(
+        dw, step_bytes / len(cfgs), (cfgs[0].batch, cfgs[0].in_feat, cfgs[0].out_feat) if gemm else None, args.steps)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(cfgs, inputs, args.cpu_seconds)
     ctx.close()
