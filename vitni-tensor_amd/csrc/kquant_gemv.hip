@@ -143,29 +143,36 @@ __device__ __forceinline__ float windows_tree(float (&wv)[N]) {
 //   stride 4:    row_bcast:15 adds row 0 into row 1 and row 2 into row 3
 //   stride 8:    row_bcast:31 adds (row0+row1) into row 3
 // The window sum ends in lane 63 and is read out once.
-template <int CTRL, int ROWMASK>
-__device__ __forceinline__ float dpp_add_f(float v) {
-    const float t = __int_as_float(
-        __builtin_amdgcn_update_dpp(__float_as_int(-0.0f), __float_as_int(v), CTRL, ROWMASK, 0xF, false));
-    return v + t;
-}
+//
+// Each step is one v_add_f32_dpp with the destination equal to the unshifted
+// operand and bound_ctrl off: a lane whose source lane is outside its row, or
+// whose row is masked off, is not written and keeps v, which is v + (-0.0)
+// bit for bit (f32 denormals are not flushed).  The s_nop 1 ahead of each
+// step covers the two wait states between a VALU write of a VGPR and a DPP
+// read of it; the one at the end covers the readlane that follows.
+#define VTQ_DPP_ADD(ctrl) "s_nop 1\n\tv_add_f32_dpp %0, %0, %0 " ctrl " bank_mask:0xf\n\t"
 __device__ __forceinline__ float window16_tree(float v) {
-    v = dpp_add_f<0x114, 0xF>(v);  // row_shr:4  (lanes 0..3 of a row add -0.0)
-    v = dpp_add_f<0x118, 0xF>(v);  // row_shr:8
-    v = dpp_add_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
-    v = dpp_add_f<0x143, 0x8>(v);  // row_bcast:31 into row 3
+    asm(VTQ_DPP_ADD("row_shr:4 row_mask:0xf")      // lanes 0..3 of a row keep v
+        VTQ_DPP_ADD("row_shr:8 row_mask:0xf")      //
+        VTQ_DPP_ADD("row_bcast:15 row_mask:0xa")   // row 0 into row 1, row 2 into row 3
+        VTQ_DPP_ADD("row_bcast:31 row_mask:0x8")   // (row0+row1) into row 3
+        "s_nop 1"
+        : "+v"(v));
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 // The same for two rows of at most 8 block slots each, row h in lanes
 // 32h..32h+31: strides 1, 2 and 4 of window16_tree; the sums end in lanes 31
 // (row 0) and 63 (row 1).
 __device__ __forceinline__ float2 window8x2_tree(float v) {
-    v = dpp_add_f<0x114, 0xF>(v);  // row_shr:4
-    v = dpp_add_f<0x118, 0xF>(v);  // row_shr:8
-    v = dpp_add_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1 and 3
+    asm(VTQ_DPP_ADD("row_shr:4 row_mask:0xf")
+        VTQ_DPP_ADD("row_shr:8 row_mask:0xf")
+        VTQ_DPP_ADD("row_bcast:15 row_mask:0xa")
+        "s_nop 1"
+        : "+v"(v));
     return make_float2(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31)),
                        __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63)));
 }
+#undef VTQ_DPP_ADD
 
 // ------------------------------------------------------- raw buffer loads
 
@@ -297,7 +304,7 @@ struct Q6K {
         uint32_t d;    // f16 bits of d
     };
     // the lane's activation: runs 8hf+t+2q (q = 0..3) of block g, with
-    // m_q = 32 * (sum of run q) to fold the code offset -32 in exactly
+    // m_q = -32 * (sum of run q) to fold the code offset -32 in exactly
     struct X {
         uint4 x1, x2, x3, x4;
         int m1, m2, m3, m4;
@@ -321,14 +328,16 @@ struct Q6K {
         r.sc = funnel16(v, tail, off);
         r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
     }
+    // Buffer loads at 2-byte-aligned offsets: the HSA runtime runs the shader
+    // memory path in unaligned mode (the compiler itself emits dwordx4 loads
+    // for byte-aligned memcpy on this target), so each 16-byte run is one
+    // load with no funnel shift.
     __device__ static void bload(Regs& r, __amdgpu_buffer_rsrc_t rs, uint32_t blk, int k) {
         const int hf = k >> 1, t = k & 1;
-        r.b0 = buf_load16_a2(rs, blk + 64 * hf + 16 * t);
-        r.b1 = buf_load16_a2(rs, blk + 64 * hf + 32 + 16 * t);
-        r.hh = buf_load16_a2(rs, blk + 128 + 32 * hf + 16 * t);
-        const uint32_t off = (blk + 192) & 3u;
-        const u32x4_a4 v = __builtin_bit_cast(u32x4_a4, __builtin_amdgcn_raw_buffer_load_b128(rs, blk + 192 - off, 0, 0));
-        r.sc = funnel16(v, buf_load2(rs, blk + 206), off);
+        r.b0 = buf_load16(rs, blk + 64 * hf + 16 * t);
+        r.b1 = buf_load16(rs, blk + 64 * hf + 32 + 16 * t);
+        r.hh = buf_load16(rs, blk + 128 + 32 * hf + 16 * t);
+        r.sc = buf_load16(rs, blk + 192);
         r.d = buf_load2(rs, blk + 208);
     }
     // activation words: element 128hf + 16t + 32q + 4i -> word 32hf + 4t + 8q + i;
@@ -341,22 +350,23 @@ struct Q6K {
         x.x3 = *reinterpret_cast<const uint4*>(xw + 16);
         x.x4 = *reinterpret_cast<const uint4*>(xw + 24);
         const int* s16 = act.s16 + b * 64 + 4 * (8 * hf + t);
-        x.m1 = 32 * s16[0];
-        x.m2 = 32 * s16[8];
-        x.m3 = 32 * s16[16];
-        x.m4 = 32 * s16[24];
+        x.m1 = -32 * s16[0];
+        x.m2 = -32 * s16[8];
+        x.m3 = -32 * s16[16];
+        x.m4 = -32 * s16[24];
         x.dx = act.d[b * 64];
     }
     // dot_q6k_q8_block (src/ops/quant.rs:995-1057): buckets 8hf+t+2q (q = 0..3)
     // are exactly one 16-element run each; (code - 32) is folded in as
-    // sum(code*x) - 32*sum(x) with the run sums from the activation pass.
+    // sum(code*x) - 32*sum(x) with the run sums from the activation pass,
+    // the second term as the starting value of the dot accumulator.
     __device__ static float part(const Regs& r, const X& x, const Lane& c, bool valid) {
         const uint32_t B0[4] = {r.b0.x, r.b0.y, r.b0.z, r.b0.w};
         const uint32_t B1[4] = {r.b1.x, r.b1.y, r.b1.z, r.b1.w};
         const uint32_t H[4] = {r.hh.x, r.hh.y, r.hh.z, r.hh.w};
         const uint32_t X1[4] = {x.x1.x, x.x1.y, x.x1.z, x.x1.w}, X2[4] = {x.x2.x, x.x2.y, x.x2.z, x.x2.w};
         const uint32_t X3[4] = {x.x3.x, x.x3.y, x.x3.z, x.x3.w}, X4[4] = {x.x4.x, x.x4.y, x.x4.z, x.x4.w};
-        int S1 = 0, S2 = 0, S3 = 0, S4 = 0;
+        int S1 = x.m1, S2 = x.m2, S3 = x.m3, S4 = x.m4;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t q1 = (B0[i] & 0x0F0F0F0Fu) | ((H[i] & 0x03030303u) << 4);
@@ -368,12 +378,11 @@ struct Q6K {
             S3 = __builtin_amdgcn_sdot4((int)q3, (int)X3[i], S3, false);
             S4 = __builtin_amdgcn_sdot4((int)q4, (int)X4[i], S4, false);
         }
-        const int sum1 = S1 - x.m1, sum2 = S2 - x.m2, sum3 = S3 - x.m3, sum4 = S4 - x.m4;
         // scales: i8 at 192 + 8hf + t + 2q -> bytes t, t+2 of dwords 2hf and 2hf+1
         const uint32_t sa = c.hf ? r.sc.z : r.sc.x, sb = c.hf ? r.sc.w : r.sc.y;
         // |sc| <= 64 and |sum| <= 16*31*127: every product fits v_mad_i32_i24
-        int acc = __mul24(sext8(sa, c.t), sum1) + __mul24(sext8(sa, c.t + 2), sum2) +
-                  __mul24(sext8(sb, c.t), sum3) + __mul24(sext8(sb, c.t + 2), sum4);
+        int acc = __mul24(sext8(sa, c.t), S1) + __mul24(sext8(sa, c.t + 2), S2) +
+                  __mul24(sext8(sb, c.t), S3) + __mul24(sext8(sb, c.t + 2), S4);
         acc = quad_sum_i(acc);
         const float d = f16_hw(r.d);
         return valid ? (d * x.dx) * (float)acc : -0.0f;
