@@ -41,6 +41,14 @@ const char *vtqrt_last_error(const vtqrt_model *m);
 /* dim, hidden, layers, heads, kv_heads, vocab, seq_len */
 int vtqrt_dims(const vtqrt_model *m, int dims[7]);
 
+/* rms_norm_slice (src/ops/rms_norm.rs:60-110) on device memory: d_y[i] =
+ * d_x[i] * scale * d_w[i], scale = 1 / sqrt(sum(x*x) / n + eps) with the
+ * sum of squares in the reference's serial order, enqueued on `stream` (a
+ * hipStream_t on the current device, NULL for the null stream).  The decode
+ * step uses the same sum (fused into the GEMV that consumes the norm).
+ * 1 <= n <= 32768; d_x, d_w, d_y 4-byte aligned. */
+int vtqrt_rms_norm_device(const float *d_x, const float *d_w, size_t n, float eps, float *d_y, void *stream);
+
 /* inference::run_quantized.  regime: VTQ_REGIME_INTEGER (std-parallel
  * build) or VTQ_REGIME_FLOAT_FUSED (default build) for the Q4_K arm.
  * logits (optional) receives (prompt_len + n_new) * vocab floats, one row per

@@ -693,6 +693,14 @@ int vtqrt_dims(const vtqrt_model* m, int dims[7]) {
     return VTQ_OK;
 }
 
+int vtqrt_rms_norm_device(const float* d_x, const float* d_w, size_t n, float eps, float* d_y, void* stream) {
+    if (!d_x || !d_w || !d_y) return VTQ_E_INVALID_ARGUMENT;
+    if (n < 1 || n > 32768) return VTQ_E_NOT_IMPLEMENTED;
+    return vtq::decode::rms_norm(d_x, d_w, (int)n, eps, d_y, static_cast<hipStream_t>(stream)) == hipSuccess
+               ? VTQ_OK
+               : VTQ_E_GPU;
+}
+
 void vtqrt_free(vtqrt_model* m) {
     if (!m) return;
     if (m->stream) (void)hipStreamSynchronize(m->stream);

@@ -37,6 +37,8 @@ def lib() -> ctypes.CDLL:
         L.vtqrt_run_recorded.restype = i
         L.vtqrt_blake3.argtypes = [vp, sz, vp]
         L.vtqrt_blake3.restype = None
+        L.vtqrt_rms_norm_device.argtypes = [vp, vp, sz, ctypes.c_float, vp, vp]
+        L.vtqrt_rms_norm_device.restype = i
         _rt = L
     return _rt
 
@@ -47,6 +49,13 @@ def blake3(data) -> bytes:
     out = (ctypes.c_uint8 * 32)()
     lib().vtqrt_blake3(d.ctypes.data if d.size else None, d.size, out)
     return bytes(out)
+
+
+def rms_norm_device(x_ptr, w_ptr, n, eps, y_ptr, stream=None) -> None:
+    """vtqrt_rms_norm_device: enqueue rms_norm_slice on device pointers."""
+    rc = lib().vtqrt_rms_norm_device(x_ptr, w_ptr, n, float(eps), y_ptr, stream)
+    if rc != 0:
+        raise RuntimeError(f"vtqrt_rms_norm_device failed with status {rc}")
 
 
 RECORD_OPS = 1
