@@ -272,25 +272,12 @@ struct Q4K {
 
 // ------------------------------------------------------------------ Q6_K
 
-// 16 bytes from a 2-byte-aligned address p, as five aligned dwords from
-// p & ~3 funnel-shifted by (p & 3) bytes.  Reads [p - (p&3), p - (p&3) + 20),
-// which for the runs used below stays inside the 210-byte block.
-__device__ __forceinline__ uint4 funnel16(u32x4_a4 v, uint32_t e, uint32_t off) {
-    return make_uint4(__builtin_amdgcn_alignbyte(v.y, v.x, off), __builtin_amdgcn_alignbyte(v.z, v.y, off),
-                      __builtin_amdgcn_alignbyte(v.w, v.z, off), __builtin_amdgcn_alignbyte(e, v.w, off));
-}
-__device__ __forceinline__ uint4 load16_a2(const uint8_t* p) {
-    // pointer arithmetic (not an integer round trip) keeps the global address
-    // space visible to the compiler: global_load, not flat_load
-    const uint32_t off = (uint32_t)(reinterpret_cast<uintptr_t>(p) & 3u);
-    const uint32_t* p4 = reinterpret_cast<const uint32_t*>(p - off);
-    return funnel16(*reinterpret_cast<const u32x4_a4*>(p4), p4[4], off);
-}
-// The same from a buffer whose base is 16-byte aligned.
-__device__ __forceinline__ uint4 buf_load16_a2(__amdgpu_buffer_rsrc_t rs, uint32_t p) {
-    const uint32_t off = p & 3u, a = p - off;
-    const u32x4_a4 v = __builtin_bit_cast(u32x4_a4, __builtin_amdgcn_raw_buffer_load_b128(rs, a, 0, 0));
-    return funnel16(v, buf_load4(rs, a + 16), off);
+// 16 bytes from a 2-byte-aligned address, as one global_load_dwordx4 (the
+// vector memory path runs in unaligned mode on this target).
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+__device__ __forceinline__ uint4 load16_u(const uint8_t* p) {
+    const u32x4_a2 v = *reinterpret_cast<const u32x4_a2*>(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 __device__ __forceinline__ int sext8(uint32_t v, int byte) { return (int)(int8_t)((v >> (8 * byte)) & 0xFFu); }
@@ -315,17 +302,14 @@ struct Q6K {
         int hf, t;
     };
     __device__ static Lane lane_consts(int k) { return Lane{k >> 1, k & 1}; }
-    // Reads stay inside the block: ql/qh runs end by byte 196, the scale
-    // dwords start at 192 - (blk&3) and two ushorts read bytes 206..209.
+    // One unaligned 16-byte load per run (see bload); every read stays
+    // inside the 210-byte block.
     __device__ static void load(Regs& r, const uint8_t* __restrict__ blk, int k) {
         const int hf = k >> 1, t = k & 1;
-        r.b0 = load16_a2(blk + 64 * hf + 16 * t);
-        r.b1 = load16_a2(blk + 64 * hf + 32 + 16 * t);
-        r.hh = load16_a2(blk + 128 + 32 * hf + 16 * t);
-        const uint32_t off = (uint32_t)(reinterpret_cast<uintptr_t>(blk + 192) & 3u);
-        const u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(blk + 192 - off);
-        const uint32_t tail = *reinterpret_cast<const uint16_t*>(blk + 206);  // bytes 206, 207
-        r.sc = funnel16(v, tail, off);
+        r.b0 = load16_u(blk + 64 * hf + 16 * t);
+        r.b1 = load16_u(blk + 64 * hf + 32 + 16 * t);
+        r.hh = load16_u(blk + 128 + 32 * hf + 16 * t);
+        r.sc = load16_u(blk + 192);
         r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
     }
     // Buffer loads at 2-byte-aligned offsets: the HSA runtime runs the shader
