@@ -24,6 +24,13 @@
  *   VTQ_E_NOT_IMPLEMENTED  Error::NotImplemented          (F16/other dtypes,
  *                          in_feat beyond the kernels' limit)
  *   VTQ_E_INVALID_ARGUMENT null pointer or context; Rust's types rule these out
+ *   VTQ_E_MALFORMED        Error::Malformed               (GGUF parse, libvtq_runtime)
+ *   VTQ_E_TRUNCATED        Error::Truncated               (GGUF parse, libvtq_runtime)
+ *   VTQ_E_OVERFLOW         Error::Overflow                (GGUF parse, libvtq_runtime)
+ *   VTQ_E_SHAPE_MISMATCH   Error::ShapeMismatch           (a norm weight whose length
+ *                          is not the model dimension, rms_norm.rs:80-85)
+ *   VTQ_E_INVALID_SHAPE    Error::InvalidShape            (empty prompt, prompt + new
+ *                          tokens past seq_len, inference.rs:301-311)
  * No entry point aborts or panics.
  *
  * Threading: a context is used by one host thread at a time (the reference's
@@ -45,6 +52,11 @@ extern "C" {
 #define VTQ_E_GPU 2
 #define VTQ_E_NOT_IMPLEMENTED 3
 #define VTQ_E_INVALID_ARGUMENT 4
+#define VTQ_E_MALFORMED 5
+#define VTQ_E_TRUNCATED 6
+#define VTQ_E_OVERFLOW 7
+#define VTQ_E_SHAPE_MISMATCH 8
+#define VTQ_E_INVALID_SHAPE 9
 
 /* GGUF tensor type tags (src/model/gguf.rs:127-139). */
 #define VTQ_TYPE_F32 0

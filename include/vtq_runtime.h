@@ -13,11 +13,17 @@
  * generated tokens and the `vitnify-receipt v2` model digest
  * (src/cert/builder.rs:458-471).
  *
- * The GGUF blob is parsed once and uploaded to device memory once; every
- * linear runs on the GPU through vtq_linear_device (include/vtq.h) on
- * device-resident weights.  The rest of the step (embedding row, RMSNorm,
- * RoPE, attention over the KV cache, SwiGLU, argmax) runs on the host in
- * the reference's operation order.
+ * The GGUF blob is parsed on the host once (every length, count and offset
+ * checked as the reference checks them; a malformed file never reaches the
+ * device) and each tensor the step reads is uploaded to device memory once.
+ * The whole decode step runs on the GPU: the embedding row, RMSNorm, the
+ * linears (the libvtq kernels, with the k-quant GEMVs of a layer fused: q|k|v
+ * in one launch, the residual adds into Wo and W2, SwiGLU into W1|W3), RoPE,
+ * attention over the KV cache and the argmax, in the reference's operation
+ * order.  Activations, the KV cache, the token sequence and the step
+ * position stay in device memory; one step is captured once in a HIP graph
+ * and replayed per position, and the host reads the tokens (and the logits
+ * history, when asked for) once at the end.
  *
  * Status codes are those of include/vtq.h; vtqrt_last_error() gives text.
  */
@@ -33,8 +39,22 @@ extern "C" {
 
 typedef struct vtqrt_model vtqrt_model;
 
-/* Parse a GGUF v2/v3 blob and upload it to HIP device `device`.  The blob is
- * copied; the caller may free it afterwards. */
+/* GgufFile::parse (level 0: src/model/gguf.rs:305-421), or the parse plus
+ * Config::from_gguf and QuantizedWeights::from_gguf (level 1:
+ * src/model/config.rs:156-213, src/model/quant_weights.rs:121-181), on the
+ * host only: no device is touched, so it runs without a GPU.  Returns VTQ_OK
+ * or the status of the first check that fails (VTQ_E_MALFORMED /
+ * VTQ_E_TRUNCATED / VTQ_E_OVERFLOW for the file, VTQ_E_INTERNAL for the
+ * model tables, as the reference's Error variants) with the reference's
+ * text in err (optional, NUL-terminated, at most err_cap bytes).  dims
+ * (optional, level 1) receives dim, hidden, layers, heads, kv_heads, vocab,
+ * seq_len.  vtqrt_load runs the same checks first. */
+int vtqrt_parse(const uint8_t *gguf, size_t len, int level, int dims[7], char *err, size_t err_cap);
+
+/* Parse a GGUF v2/v3 blob (vtqrt_parse level 1) and upload the tensors the
+ * decode step reads to HIP device `device`.  The blob is copied; the caller
+ * may free it afterwards.  On failure *out still holds a model whose
+ * vtqrt_last_error() explains it; free it with vtqrt_free. */
 int vtqrt_load(int device, const uint8_t *gguf, size_t len, vtqrt_model **out);
 void vtqrt_free(vtqrt_model *m);
 const char *vtqrt_last_error(const vtqrt_model *m);
@@ -49,14 +69,34 @@ int vtqrt_dims(const vtqrt_model *m, int dims[7]);
  * 1 <= n <= 32768; d_x, d_w, d_y 4-byte aligned. */
 int vtqrt_rms_norm_device(const float *d_x, const float *d_w, size_t n, float eps, float *d_y, void *stream);
 
+/* The single-precision libm functions the decode step evaluates on the
+ * device (the `libm = "0.2"` crate's expf, sqrtf, cosf, sinf, powf; RoPE,
+ * softmax, SwiGLU and RMSNorm call them, src/model/forward_quantized.rs:
+ * 423-559, src/ops/rms_norm.rs:102), over d_x[0..n): d_y[7i + k] = f_k(d_x[i])
+ * for the seven evaluations of the reference's transcendental sweep in its
+ * order (tests/transcendental_determinism.rs:34-42): expf(x), sqrtf(|x|),
+ * cosf(x), sinf(x), powf(1e4, x/64), powf(1e6, x/64), 1/(1+expf(-x)).
+ * Enqueued on `stream`; it exists so the device code can be pinned by the
+ * reference's PINNED_TRANSCENDENTAL hash.  n < 2^31 / 7. */
+int vtqrt_transcendentals_device(const float *d_x, size_t n, float *d_y, void *stream);
+
 /* inference::run_quantized.  regime: VTQ_REGIME_INTEGER (std-parallel
  * build) or VTQ_REGIME_FLOAT_FUSED (default build) for the Q4_K arm.
  * logits (optional) receives (prompt_len + n_new) * vocab floats, one row per
- * decode step; tokens receives the n_new generated ids; digest the v2 model
- * digest.  weights_hash is BLAKE3 of the whole GGUF blob (vtqrt_blake3). */
+ * decode step; tokens receives the n_new generated ids; digest the
+ * `vitnify-receipt v2` model digest (compute_digest, src/cert/builder.rs:
+ * 458-471); digest_v1 (optional) the frozen `vitnify-receipt v1` digest of
+ * the same cert (compute_digest_v1, :476-487), which vitni-receipt prints
+ * as model_digest_v1 (src/bin/vitni-receipt.rs:40-55).  weights_hash is
+ * BLAKE3 of the whole GGUF blob (vtqrt_blake3).  Errors, in the reference's
+ * order: VTQ_E_INVALID_SHAPE for an empty prompt or prompt_len + n_new past
+ * seq_len; then what step 0 would report (embedding_row's texts, a norm
+ * weight of the wrong length as VTQ_E_SHAPE_MISMATCH, each linear's
+ * linear_dispatch error); then a prompt or generated token past the
+ * embedding table.  Nothing is launched until these checks pass. */
 int vtqrt_run(vtqrt_model *m, int regime, const char *model_id, const uint8_t weights_hash[32],
               const uint32_t *prompt, int prompt_len, int n_new, float *logits, uint32_t *tokens,
-              uint8_t digest[32]);
+              uint8_t digest[32], uint8_t digest_v1[32]);
 
 /* run_quantized with a PerOpRecorder and/or a PerActivationRecorder attached
  * to every step (src/model/forward_quantized.rs:64-132, :260-284,

@@ -100,8 +100,12 @@ def lib() -> ctypes.CDLL:
     L.vtqo_model_free.restype = None
     L.vtqo_model_dims.argtypes = [vp, vp]
     L.vtqo_model_dims.restype = None
-    L.vtqo_run_quantized.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, i, vp, vp, vp, msgp]
+    L.vtqo_run_quantized.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, i, vp, vp, vp, vp, msgp]
     L.vtqo_run_quantized.restype = i
+    L.vtqo_gguf_parse.argtypes = [vp, sz, i, msgp]
+    L.vtqo_gguf_parse.restype = i
+    L.vtqo_digest_v1_full.argtypes = [i, vp, vp, vp, i, vp, vp, vp, sz, vp, sz, vp, vp]
+    L.vtqo_digest_v1_full.restype = None
     _lib = L
     return L
 
@@ -408,6 +412,25 @@ def _fields(items):
     return names, datas, lens, bufs
 
 
+def gguf_parse(blob, level=0):
+    """GgufFile::parse (level 0) or parse + Config / QuantizedWeights (level
+    1): (status, message); status 0 is Ok, else the include/vtq.h code of the
+    reference's Error variant."""
+    b = _u8(blob)
+    msg = ctypes.c_char_p()
+    rc = lib().vtqo_gguf_parse(_ptr(b) if b.size else None, b.size, level, ctypes.byref(msg))
+    return rc, (msg.value.decode() if msg.value else "")
+
+
+def digest_v1(inputs, outputs) -> str:
+    """Frozen vitnify-receipt v1 digest of [(name, bytes)] inputs and outputs."""
+    ni, di, li, keep_i = _fields(inputs)
+    no, do, lo, keep_o = _fields(outputs)
+    out = (ctypes.c_uint8 * 32)()
+    lib().vtqo_digest_v1_full(len(inputs), ni, di, li, len(outputs), no, do, lo, 0, None, 0, None, out)
+    return bytes(out).hex()
+
+
 def digest_v2(inputs, outputs) -> str:
     """vitnify-receipt v2 digest of [(name, bytes)] inputs and outputs."""
     ni, di, li, keep_i = _fields(inputs)
@@ -443,9 +466,11 @@ class ActRecord(ctypes.Structure):
 
 
 class Model:
-    """GGUF model for inference::run_quantized (the blob must stay alive)."""
+    """GGUF model for inference::run_quantized (the blob must stay alive).
+    After run(), digest_v1 holds the frozen v1 digest of the same cert."""
 
     def __init__(self, blob):
+        self.digest_v1 = None
         self.blob = _u8(blob)
         self.handle = ctypes.c_void_p()
         msg = ctypes.c_char_p()
@@ -462,10 +487,13 @@ class Model:
         tokens = np.zeros(max(1, n_new), dtype=np.uint32)
         logits = np.zeros((prompt.size + n_new) * self.vocab, dtype=np.float32) if want_logits else None
         digest = (ctypes.c_uint8 * 32)()
+        digest_v1 = (ctypes.c_uint8 * 32)()
         msg = ctypes.c_char_p()
         rc = lib().vtqo_run_quantized(self.handle, regime, model_id.encode(), _ptr(wh), _ptr(prompt), prompt.size,
-                                      n_new, threads, _ptr(logits), _ptr(tokens), digest, ctypes.byref(msg))
+                                      n_new, threads, _ptr(logits), _ptr(tokens), digest, digest_v1,
+                                      ctypes.byref(msg))
         _check(rc, msg)
+        self.digest_v1 = bytes(digest_v1).hex()  # compute_digest_v1 of the same cert
         if logits is not None:
             logits = logits.reshape(prompt.size + n_new, self.vocab)
         return tokens[:n_new], bytes(digest).hex(), logits

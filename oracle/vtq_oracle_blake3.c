@@ -213,6 +213,22 @@ static void write_activation(vtqo_blake3* h, const vtqo_act_record* a) {
     vtqo_blake3_update(h, a->tensor_hash, 32);
 }
 
+/* write_sections (builder.rs:491-519): identical in v1 and v2 */
+static void sections(vtqo_blake3* h, int n_in, const char* const* in_names, const uint8_t* const* in_data,
+                     const size_t* in_lens, int n_out, const char* const* out_names, const uint8_t* const* out_data,
+                     const size_t* out_lens, size_t n_ops, const vtqo_op_record* ops, size_t n_acts,
+                     const vtqo_act_record* acts) {
+    leb128(h, (uint64_t)n_in);
+    for (int i = 0; i < n_in; i++) field(h, in_names[i], in_data[i], in_lens[i]);
+    leb128(h, (uint64_t)n_out);
+    for (int i = 0; i < n_out; i++) field(h, out_names[i], out_data[i], out_lens[i]);
+    leb128(h, (uint64_t)n_ops);
+    for (size_t i = 0; i < n_ops; i++) write_op(h, &ops[i]);
+    leb128(h, (uint64_t)n_acts);
+    for (size_t i = 0; i < n_acts; i++) write_activation(h, &acts[i]);
+    leb128(h, 0);  /* interventions */
+}
+
 void vtqo_digest_v2_full(int n_in, const char* const* in_names, const uint8_t* const* in_data, const size_t* in_lens,
                          int n_out, const char* const* out_names, const uint8_t* const* out_data,
                          const size_t* out_lens, size_t n_ops, const vtqo_op_record* ops, size_t n_acts,
@@ -223,15 +239,19 @@ void vtqo_digest_v2_full(int n_in, const char* const* in_names, const uint8_t* c
     vtqo_blake3_update(&h, "vitnify-receipt v2\x00", 19);
     leb128(&h, sizeof kRegime - 1);
     vtqo_blake3_update(&h, kRegime, sizeof kRegime - 1);
-    leb128(&h, (uint64_t)n_in);
-    for (int i = 0; i < n_in; i++) field(&h, in_names[i], in_data[i], in_lens[i]);
-    leb128(&h, (uint64_t)n_out);
-    for (int i = 0; i < n_out; i++) field(&h, out_names[i], out_data[i], out_lens[i]);
-    leb128(&h, (uint64_t)n_ops);
-    for (size_t i = 0; i < n_ops; i++) write_op(&h, &ops[i]);
-    leb128(&h, (uint64_t)n_acts);
-    for (size_t i = 0; i < n_acts; i++) write_activation(&h, &acts[i]);
-    leb128(&h, 0);  /* interventions */
+    sections(&h, n_in, in_names, in_data, in_lens, n_out, out_names, out_data, out_lens, n_ops, ops, n_acts, acts);
+    vtqo_blake3_final(&h, out);
+}
+
+/* compute_digest_v1 (builder.rs:476-487): the frozen domain, no regime */
+void vtqo_digest_v1_full(int n_in, const char* const* in_names, const uint8_t* const* in_data, const size_t* in_lens,
+                         int n_out, const char* const* out_names, const uint8_t* const* out_data,
+                         const size_t* out_lens, size_t n_ops, const vtqo_op_record* ops, size_t n_acts,
+                         const vtqo_act_record* acts, uint8_t out[32]) {
+    vtqo_blake3 h;
+    vtqo_blake3_init(&h);
+    vtqo_blake3_update(&h, "vitnify-receipt v1\x00", 19);
+    sections(&h, n_in, in_names, in_data, in_lens, n_out, out_names, out_data, out_lens, n_ops, ops, n_acts, acts);
     vtqo_blake3_final(&h, out);
 }
 

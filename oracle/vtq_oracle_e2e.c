@@ -29,27 +29,83 @@
 
 /* ---------------------------------------------------------------- GGUF */
 
+/* Status codes of the parse and the model tables, as the reference's Error
+ * variants (the numbering of include/vtq.h). */
+enum { E_INTERNAL = 1, E_NOT_IMPLEMENTED = 3, E_MALFORMED = 5, E_TRUNCATED = 6, E_OVERFLOW = 7,
+       E_SHAPE_MISMATCH = 8, E_INVALID_SHAPE = 9 };
+
 enum { T_U8 = 0, T_I8, T_U16, T_I16, T_U32, T_I32, T_F32, T_BOOL, T_STR, T_ARR, T_U64, T_I64, T_F64 };
 
+/* Cursor (src/model/gguf.rs:483-617): the first error sticks */
 typedef struct {
     const uint8_t* p;
     size_t len, pos;
-    int bad;
+    int code;
+    const char* msg;
 } cur_t;
 
-static int need(cur_t* c, size_t n) {
-    if (c->bad || c->len - c->pos < n) {
-        c->bad = 1;
-        return 0;
+static int cfail(cur_t* c, int code, const char* msg) {
+    if (!c->code) {
+        c->code = code;
+        c->msg = msg;
+    }
+    return 0;
+}
+/* read_n: pos + n overflowing is Overflow, past the end Truncated */
+static int read_n(cur_t* c, uint64_t n, const uint8_t** out) {
+    if (c->code) return 0;
+    if (n > SIZE_MAX - c->pos) return cfail(c, E_OVERFLOW, "gguf: read past end (overflow)");
+    if (c->pos + n > c->len) return cfail(c, E_TRUNCATED, "gguf: read past end");
+    *out = c->p + c->pos;
+    c->pos += (size_t)n;
+    return 1;
+}
+static int rd(cur_t* c, int bytes, uint64_t* v) {
+    const uint8_t* s;
+    if (!read_n(c, (uint64_t)bytes, &s)) return 0;
+    uint64_t r = 0;
+    for (int i = 0; i < bytes; i++) r |= (uint64_t)s[i] << (8 * i);
+    *v = r;
+    return 1;
+}
+/* core::str::from_utf8's acceptance (RFC 3629 well-formed sequences) */
+static int utf8_valid(const uint8_t* s, size_t n) {
+    for (size_t i = 0; i < n;) {
+        uint32_t cp;
+        int k;
+        if (s[i] < 0x80) {
+            i++;
+            continue;
+        } else if ((s[i] & 0xE0) == 0xC0) {
+            cp = s[i] & 0x1F;
+            k = 1;
+        } else if ((s[i] & 0xF0) == 0xE0) {
+            cp = s[i] & 0x0F;
+            k = 2;
+        } else if ((s[i] & 0xF8) == 0xF0) {
+            cp = s[i] & 0x07;
+            k = 3;
+        } else {
+            return 0;
+        }
+        if (n - i <= (size_t)k) return 0;
+        for (int j = 1; j <= k; j++) {
+            if ((s[i + j] & 0xC0) != 0x80) return 0;
+            cp = cp << 6 | (s[i + j] & 0x3F);
+        }
+        static const uint32_t kMin[4] = {0, 0x80, 0x800, 0x10000};
+        if (cp < kMin[k] || cp > 0x10FFFF || (cp >= 0xD800 && cp <= 0xDFFF)) return 0;
+        i += (size_t)k + 1;
     }
     return 1;
 }
-static uint64_t rd(cur_t* c, int bytes) {
-    if (!need(c, (size_t)bytes)) return 0;
-    uint64_t v = 0;
-    for (int i = 0; i < bytes; i++) v |= (uint64_t)c->p[c->pos + i] << (8 * i);
-    c->pos += (size_t)bytes;
-    return v;
+/* read_string: u64 length, at most 1 MiB, UTF-8 */
+static int rd_str(cur_t* c, const uint8_t** s, uint64_t* n) {
+    if (!rd(c, 8, n)) return 0;
+    if (*n > (1u << 20)) return cfail(c, E_MALFORMED, "gguf: string length > 1 MiB");
+    if (!read_n(c, *n, s)) return 0;
+    if (!utf8_valid(*s, (size_t)*n)) return cfail(c, E_MALFORMED, "gguf: non-UTF8 string");
+    return 1;
 }
 static int scalar_size(uint32_t t) {
     switch (t) {
@@ -62,7 +118,8 @@ static int scalar_size(uint32_t t) {
 }
 
 typedef struct {
-    char key[96];
+    const uint8_t* key;
+    uint64_t key_len;
     uint32_t type;
     uint64_t num;           /* integer value / f32 bits */
     const uint8_t* str;     /* string bytes */
@@ -70,54 +127,72 @@ typedef struct {
 } kv_t;
 
 typedef struct {
-    char name[96];
+    const uint8_t* name;
+    uint64_t name_len;
     uint32_t type;
-    uint64_t numel;
-    const uint8_t* bytes;
+    uint64_t shape[8];
+    uint32_t n_dims;
+    uint64_t offset;        /* relative to the data section */
+    const uint8_t* bytes;   /* absolute */
     size_t nbytes;
 } tinfo_t;
 
-static int skip_value(cur_t* c, uint32_t t, kv_t* out) {
-    if (t == T_STR) {
-        uint64_t n = rd(c, 8);
-        if (!need(c, n)) return 0;
-        if (out) {
-            out->str = c->p + c->pos;
-            out->str_len = n;
+/* read_value (gguf.rs:528-615) */
+static int rd_value(cur_t* c, uint32_t t, kv_t* out) {
+    if (t == T_STR) return rd_str(c, &out->str, &out->str_len);
+    if (t == T_ARR) {
+        uint64_t et, n;
+        if (!rd(c, 4, &et)) return 0;
+        if (et > T_F64) return cfail(c, E_MALFORMED, "gguf: bad array elem type");
+        if (et == T_ARR) return cfail(c, E_MALFORMED, "gguf: nested arrays not supported");
+        if (!rd(c, 8, &n)) return 0;
+        out->str_len = n;
+        if (et == T_STR) {
+            for (uint64_t i = 0; i < n; i++) {
+                uint64_t sl;
+                if (!rd(c, 8, &sl)) return 0;
+                if (sl > SIZE_MAX - c->pos) return cfail(c, E_OVERFLOW, "gguf: array string overflow");
+                if (c->pos + sl > c->len) return cfail(c, E_TRUNCATED, "gguf: array string past end");
+                c->pos += (size_t)sl;
+            }
+            return 1;
         }
-        c->pos += n;
+        const uint64_t es = (uint64_t)scalar_size((uint32_t)et);
+        if (n > UINT64_MAX / es) return cfail(c, E_OVERFLOW, "gguf: array byte total overflow");
+        const uint64_t total = n * es;
+        if (total > SIZE_MAX - c->pos) return cfail(c, E_OVERFLOW, "gguf: array end overflow");
+        if (c->pos + total > c->len) return cfail(c, E_TRUNCATED, "gguf: array past end of buffer");
+        c->pos += (size_t)total;
         return 1;
     }
-    if (t == T_ARR) {
-        uint32_t et = (uint32_t)rd(c, 4);
-        uint64_t n = rd(c, 8);
-        if (out) out->str_len = n;
-        for (uint64_t i = 0; i < n && !c->bad; i++)
-            if (!skip_value(c, et, NULL)) return 0;
-        return !c->bad;
-    }
-    int s = scalar_size(t);
-    if (!s) {
-        c->bad = 1;
-        return 0;
-    }
-    uint64_t v = rd(c, s);
-    if (out) out->num = v;
-    return !c->bad;
+    return rd(c, scalar_size(t), &out->num);
 }
 
-static size_t bytes_for(uint32_t t, uint64_t numel, int* ok) {
-    *ok = 1;
+/* GgufTensorType::bytes_for_numel (gguf.rs:144-214) */
+static int bytes_for(uint32_t t, uint64_t numel, uint64_t* out, const char** msg) {
+    uint64_t blk, bb;
+    const char *nm, *ov;
     switch (t) {
-    case 0: return (size_t)numel * 4;
-    case 1: return (size_t)numel * 2;
-    case 2: if (numel % 32) break; return (size_t)(numel / 32) * 18;
-    case 6: if (numel % 32) break; return (size_t)(numel / 32) * 22;
-    case 8: if (numel % 32) break; return (size_t)(numel / 32) * 34;
-    case 12: if (numel % 256) break; return (size_t)(numel / 256) * 144;
-    case 14: if (numel % 256) break; return (size_t)(numel / 256) * 210;
+    case 0: blk = 1; bb = 4; nm = NULL; ov = "gguf: F32 byte size overflow"; break;
+    case 1: blk = 1; bb = 2; nm = NULL; ov = "gguf: F16 byte size overflow"; break;
+    case 2: blk = 32; bb = 18; nm = "gguf: Q4_0 tensor numel not a multiple of 32"; ov = "gguf: Q4_0 byte size overflow"; break;
+    case 8: blk = 32; bb = 34; nm = "gguf: Q8_0 tensor numel not a multiple of 32"; ov = "gguf: Q8_0 byte size overflow"; break;
+    case 6: blk = 32; bb = 22; nm = "gguf: Q5_0 tensor numel not a multiple of 32"; ov = "gguf: Q5_0 byte size overflow"; break;
+    case 12: blk = 256; bb = 144; nm = "gguf: Q4_K tensor numel not a multiple of 256"; ov = "gguf: Q4_K byte size overflow"; break;
+    case 14: blk = 256; bb = 210; nm = "gguf: Q6_K tensor numel not a multiple of 256"; ov = "gguf: Q6_K byte size overflow"; break;
+    default:
+        *msg = "gguf: byte size unknown for unsupported ggml_type";
+        return E_MALFORMED;
     }
-    *ok = 0;
+    if (numel % blk) {
+        *msg = nm;
+        return E_MALFORMED;
+    }
+    if (numel / blk > UINT64_MAX / bb) {
+        *msg = ov;
+        return E_OVERFLOW;
+    }
+    *out = numel / blk * bb;
     return 0;
 }
 
@@ -129,9 +204,15 @@ typedef struct {
     size_t len;
 } qt_t;
 
+/* an F32 tensor: its values and their count (norms and biases are taken at
+ * whatever length the file gives; the step checks or zips them) */
 typedef struct {
-    const float *rms_att, *rms_ffn;
-    const float *bq, *bk, *bv;
+    const float* v;
+    size_t n;
+} f32v_t;
+
+typedef struct {
+    f32v_t rms_att, rms_ffn, bq, bk, bv;
     qt_t wq, wk, wv, wo, w1, w2, w3;
 } layer_t;
 
@@ -140,31 +221,36 @@ struct vtqo_model {
     float rope_theta, rms_eps;
     int rope_neox;
     qt_t tok_embd, wcls;
-    const float* rms_final;
+    f32v_t rms_final;
     layer_t* layers;
     kv_t* kvs;
     size_t n_kv;
     tinfo_t* tensors;
     size_t n_tensors;
+    uint8_t* aligned;  /* a 16-byte-aligned copy of the blob when the caller's is not */
 };
 
+static int key_is(const uint8_t* k, uint64_t kl, const char* s) { return kl == strlen(s) && !memcmp(k, s, kl); }
+
+/* BTreeMap::insert: the last of repeated keys / names wins */
 static const kv_t* find_kv(const vtqo_model* m, const char* key) {
-    for (size_t i = 0; i < m->n_kv; i++)
-        if (!strcmp(m->kvs[i].key, key)) return &m->kvs[i];
+    for (size_t i = m->n_kv; i-- > 0;)
+        if (key_is(m->kvs[i].key, m->kvs[i].key_len, key)) return &m->kvs[i];
     return NULL;
 }
 static const tinfo_t* find_t(const vtqo_model* m, const char* name) {
-    for (size_t i = 0; i < m->n_tensors; i++)
-        if (!strcmp(m->tensors[i].name, name)) return &m->tensors[i];
+    for (size_t i = m->n_tensors; i-- > 0;)
+        if (key_is(m->tensors[i].name, m->tensors[i].name_len, name)) return &m->tensors[i];
     return NULL;
 }
-static int read_usize(const vtqo_model* m, const char* key, int* out) {
+/* read_u32_loose (config.rs:171-181) */
+static int read_usize(const vtqo_model* m, const char* key, uint64_t* out) {
     const kv_t* v = find_kv(m, key);
     if (!v) return 0;
     switch (v->type) {
-    case T_U32: case T_U64: *out = (int)v->num; return 1;
-    case T_I32: if ((int32_t)v->num < 0) return 0; *out = (int)(int32_t)v->num; return 1;
-    case T_I64: if ((int64_t)v->num < 0) return 0; *out = (int)(int64_t)v->num; return 1;
+    case T_U32: case T_U64: *out = v->num; return 1;
+    case T_I32: if ((int32_t)(uint32_t)v->num < 0) return 0; *out = (uint64_t)(int32_t)(uint32_t)v->num; return 1;
+    case T_I64: if ((int64_t)v->num < 0) return 0; *out = v->num; return 1;
     }
     return 0;
 }
@@ -176,191 +262,301 @@ static float read_f32_meta(const vtqo_model* m, const char* key, float def) {
     memcpy(&f, &b, 4);
     return f;
 }
-static int get_qt(const vtqo_model* m, const char* name, qt_t* out) {
-    const tinfo_t* t = find_t(m, name);
-    if (!t) return 0;
-    out->dtype = (int)t->type;
-    out->w = t->bytes;
-    out->len = t->nbytes;
-    return 1;
-}
-static const float* get_f32(const vtqo_model* m, const char* name, size_t want) {
-    const tinfo_t* t = find_t(m, name);
-    if (!t || t->type != 0 || t->nbytes != want * 4) return NULL;
-    return (const float*)t->bytes;
-}
 
 void vtqo_model_free(vtqo_model* m) {
     if (!m) return;
     free(m->layers);
     free(m->kvs);
     free(m->tensors);
+    free(m->aligned);
     free(m);
+}
+
+/* GgufFile::parse (gguf.rs:305-421) into m->kvs / m->tensors */
+static int gguf_parse(vtqo_model* m, const uint8_t* blob, size_t len, const char** msg) {
+    cur_t c = {blob, len, 0, 0, NULL};
+    const uint8_t* magic;
+    uint64_t version, n_t, n_kv;
+#define BAD() do { *msg = c.msg; return c.code; } while (0)
+    if (!read_n(&c, 4, &magic)) BAD();
+    if (memcmp(magic, "GGUF", 4)) {
+        *msg = "gguf: bad magic (not 'GGUF')";
+        return E_MALFORMED;
+    }
+    if (!rd(&c, 4, &version)) BAD();
+    if (version != 2 && version != 3) {
+        *msg = "gguf: unsupported version (only v2/v3 supported)";
+        return E_MALFORMED;
+    }
+    if (!rd(&c, 8, &n_t) || !rd(&c, 8, &n_kv)) BAD();
+    /* each metadata pair takes >= 12 bytes and each tensor record >= 24:
+     * the arrays grow only with what the blob holds */
+    size_t cap = 0;
+    for (uint64_t i = 0; i < n_kv; i++) {
+        kv_t kv;
+        memset(&kv, 0, sizeof kv);
+        uint64_t vt;
+        if (!rd_str(&c, &kv.key, &kv.key_len) || !rd(&c, 4, &vt)) BAD();
+        if (vt > T_F64) {
+            *msg = "gguf: unknown value type";
+            return E_MALFORMED;
+        }
+        kv.type = (uint32_t)vt;
+        if (!rd_value(&c, kv.type, &kv)) BAD();
+        if (m->n_kv == cap) {
+            cap = cap ? 2 * cap : 16;
+            kv_t* p = (kv_t*)realloc(m->kvs, cap * sizeof *p);
+            if (!p) {
+                *msg = "out of memory";
+                return E_INTERNAL;
+            }
+            m->kvs = p;
+        }
+        m->kvs[m->n_kv++] = kv;
+    }
+    cap = 0;
+    for (uint64_t i = 0; i < n_t; i++) {
+        tinfo_t t;
+        memset(&t, 0, sizeof t);
+        uint64_t nd, ty;
+        if (!rd_str(&c, &t.name, &t.name_len) || !rd(&c, 4, &nd)) BAD();
+        if (nd > 8) {
+            *msg = "gguf: tensor rank > 8 (sanity bound)";
+            return E_MALFORMED;
+        }
+        t.n_dims = (uint32_t)nd;
+        for (uint32_t d = 0; d < t.n_dims; d++)
+            if (!rd(&c, 8, &t.shape[d])) BAD();
+        if (!rd(&c, 4, &ty) || !rd(&c, 8, &t.offset)) BAD();
+        t.type = (uint32_t)ty;
+        if (m->n_tensors == cap) {
+            cap = cap ? 2 * cap : 16;
+            tinfo_t* p = (tinfo_t*)realloc(m->tensors, cap * sizeof *p);
+            if (!p) {
+                *msg = "out of memory";
+                return E_INTERNAL;
+            }
+            m->tensors = p;
+        }
+        m->tensors[m->n_tensors++] = t;
+    }
+#undef BAD
+    const kv_t* al = find_kv(m, "general.alignment");
+    const uint64_t alignment = (al && al->type == T_U32) ? al->num : 32;
+    if (alignment == 0) {
+        *msg = "gguf: general.alignment is zero";
+        return E_MALFORMED;
+    }
+    const uint64_t q = c.pos / alignment + (c.pos % alignment != 0);
+    if (q > UINT64_MAX / alignment) {
+        *msg = "gguf: alignment padding overflow";
+        return E_OVERFLOW;
+    }
+    const uint64_t base = q * alignment;
+    for (size_t i = 0; i < m->n_tensors; i++) {
+        tinfo_t* t = &m->tensors[i];
+        uint64_t numel = 1, nb;
+        for (uint32_t d = 0; d < t->n_dims; d++) {
+            if (t->shape[d] && numel > UINT64_MAX / t->shape[d]) {
+                *msg = "gguf: shape product overflows u64";
+                return E_OVERFLOW;
+            }
+            numel *= t->shape[d];
+        }
+        const int rc = bytes_for(t->type, numel, &nb, msg);
+        if (rc) return rc;
+        if (t->offset > UINT64_MAX - base) {
+            *msg = "gguf: tensor offset overflow";
+            return E_OVERFLOW;
+        }
+        const uint64_t start = base + t->offset;
+        if (nb > UINT64_MAX - start) {
+            *msg = "gguf: tensor end overflow";
+            return E_OVERFLOW;
+        }
+        if (start + nb > len) {
+            *msg = "gguf: tensor extends past end of file";
+            return E_TRUNCATED;
+        }
+        t->bytes = blob + start;
+        t->nbytes = (size_t)nb;
+    }
+    return 0;
+}
+
+static int get_qt(const vtqo_model* m, const char* name, qt_t* out, const char** msg) {
+    const tinfo_t* t = find_t(m, name);
+    if (!t) {
+        *msg = "gguf: required Llama tensor not found";
+        return E_INTERNAL;
+    }
+    out->dtype = (int)t->type;
+    out->w = t->bytes;
+    out->len = t->nbytes;
+    return 0;
+}
+/* read_f32_tensor / read_f32_tensor_opt (quant_weights.rs:222-272) */
+static int get_f32(const vtqo_model* m, const char* name, int optional, f32v_t* out, const char** msg) {
+    const tinfo_t* t = find_t(m, name);
+    if (!t) {
+        if (optional) return 0;
+        *msg = "gguf: required Llama tensor not found";
+        return E_INTERNAL;
+    }
+    if (t->type != 0) {
+        *msg = optional ? "gguf: expected F32 bias tensor" : "gguf: expected F32 norm-weight tensor, got something else";
+        return E_INTERNAL;
+    }
+    out->v = (const float*)(const void*)t->bytes;
+    out->n = t->nbytes / 4;
+    return 0;
+}
+
+/* Config::from_gguf (config.rs:156-213) + QuantizedWeights::from_gguf
+ * (quant_weights.rs:121-181) */
+static int describe(vtqo_model* m, const char** msg) {
+    const kv_t* a = find_kv(m, "general.architecture");
+    char arch[160], key[256];
+    if (!a || a->type != T_STR) {
+        *msg = "gguf: missing 'general.architecture' metadata";
+        return E_INTERNAL;
+    }
+    /* a longer name cannot match a metadata key of this build's lookups */
+    const size_t al = a->str_len < sizeof arch - 1 ? (size_t)a->str_len : sizeof arch - 1;
+    memcpy(arch, a->str, al);
+    arch[al] = 0;
+    uint64_t v[7];
+    static const char* const kKey[7] = {"embedding_length", "feed_forward_length", "block_count",
+                                        "attention.head_count", "attention.head_count_kv", "context_length",
+                                        "vocab_size"};
+    for (int i = 0; i < 7; i++) {
+        if (i == 6) {
+            const kv_t* toks = find_kv(m, "tokenizer.ggml.tokens");
+            if (toks && toks->type == T_ARR) {
+                v[6] = toks->str_len;
+                break;
+            }
+        }
+        snprintf(key, sizeof key, "%s.%s", arch, kKey[i]);
+        if (!read_usize(m, key, &v[i])) {
+            if (i == 4) {  /* head_count_kv: missing or unusable falls back to n_heads */
+                v[4] = v[3];
+                continue;
+            }
+            *msg = "gguf: numeric metadata missing or wrong type";
+            return E_INTERNAL;
+        }
+    }
+    for (int i = 0; i < 7; i++)
+        if (v[i] > 0x7FFFFFFFu) {
+            *msg = "vtq: model dimension above INT_MAX";
+            return E_NOT_IMPLEMENTED;
+        }
+    m->dim = (int)v[0];
+    m->hidden = (int)v[1];
+    m->n_layers = (int)v[2];
+    m->n_heads = (int)v[3];
+    m->n_kv_heads = (int)v[4];
+    m->seq_len = (int)v[5];
+    m->vocab = (int)v[6];
+    m->shared = find_t(m, "output.weight") == NULL;
+    int rc;
+    if ((rc = get_qt(m, "token_embd.weight", &m->tok_embd, msg)) ||
+        (rc = get_f32(m, "output_norm.weight", 0, &m->rms_final, msg)))
+        return rc;
+    if (!m->shared) get_qt(m, "output.weight", &m->wcls, msg);
+    snprintf(key, sizeof key, "%s.rope.freq_base", arch);
+    m->rope_theta = read_f32_meta(m, key, 10000.0f);
+    snprintf(key, sizeof key, "%s.attention.layer_norm_rms_epsilon", arch);
+    m->rms_eps = read_f32_meta(m, key, 1e-5f);
+    m->rope_neox = key_is(a->str, a->str_len, "qwen2");
+    /* layers only while their tensors exist (a huge block_count fails at the
+     * first missing name, not at an allocation) */
+    size_t cap = 0;
+    for (int l = 0; l < m->n_layers; l++) {
+        layer_t L;
+        memset(&L, 0, sizeof L);
+        char nm[64];
+#define F32(field, suffix, opt)                                                 \
+    snprintf(nm, sizeof nm, "blk.%d.%s", l, suffix);                            \
+    if ((rc = get_f32(m, nm, opt, &L.field, msg))) return rc;
+#define QT(field, suffix)                                                       \
+    snprintf(nm, sizeof nm, "blk.%d.%s", l, suffix);                            \
+    if ((rc = get_qt(m, nm, &L.field, msg))) return rc;
+        F32(rms_att, "attn_norm.weight", 0)
+        QT(wq, "attn_q.weight")
+        QT(wk, "attn_k.weight")
+        QT(wv, "attn_v.weight")
+        QT(wo, "attn_output.weight")
+        F32(rms_ffn, "ffn_norm.weight", 0)
+        QT(w1, "ffn_gate.weight")
+        QT(w2, "ffn_down.weight")
+        QT(w3, "ffn_up.weight")
+        F32(bq, "attn_q.bias", 1)
+        F32(bk, "attn_k.bias", 1)
+        F32(bv, "attn_v.bias", 1)
+#undef F32
+#undef QT
+        if ((size_t)l == cap) {
+            cap = cap ? 2 * cap : 8;
+            layer_t* p = (layer_t*)realloc(m->layers, cap * sizeof *p);
+            if (!p) {
+                *msg = "out of memory";
+                return E_INTERNAL;
+            }
+            m->layers = p;
+        }
+        m->layers[l] = L;
+    }
+    if (m->dim <= 0 || m->n_heads <= 0 || m->n_kv_heads <= 0 || m->dim % m->n_heads || m->n_heads % m->n_kv_heads) {
+        *msg = "vtq: unsupported head layout (heads and kv_heads must tile dim)";
+        return E_NOT_IMPLEMENTED;
+    }
+    return 0;
+}
+
+int vtqo_gguf_parse(const uint8_t* blob, size_t len, int level, const char** msg) {
+    vtqo_model* m = (vtqo_model*)calloc(1, sizeof *m);
+    if (!m) {
+        *msg = "out of memory";
+        return E_INTERNAL;
+    }
+    static const uint8_t kEmpty[1] = {0};
+    *msg = "";
+    int rc = gguf_parse(m, blob ? blob : kEmpty, len, msg);
+    if (!rc && level > 0) rc = describe(m, msg);
+    vtqo_model_free(m);
+    return rc;
 }
 
 int vtqo_model_load(const uint8_t* blob, size_t len, vtqo_model** out, const char** msg) {
     *out = NULL;
-    cur_t c = {blob, len, 0, 0};
-    if (!need(&c, 4) || memcmp(blob, "GGUF", 4)) {
-        *msg = "gguf: bad magic (not 'GGUF')";
-        return 1;
-    }
-    c.pos = 4;
-    uint32_t version = (uint32_t)rd(&c, 4);
-    if (version != 2 && version != 3) {
-        *msg = "gguf: unsupported version (only v2/v3 supported)";
-        return 1;
-    }
-    uint64_t n_t = rd(&c, 8), n_kv = rd(&c, 8);
-    if (c.bad || n_kv > len || n_t > len) {
-        *msg = "gguf: truncated header";
-        return 1;
-    }
+    *msg = "";
     vtqo_model* m = (vtqo_model*)calloc(1, sizeof *m);
-    m->kvs = (kv_t*)calloc(n_kv ? n_kv : 1, sizeof(kv_t));
-    m->tensors = (tinfo_t*)calloc(n_t ? n_t : 1, sizeof(tinfo_t));
-    for (uint64_t i = 0; i < n_kv; i++) {
-        uint64_t kl = rd(&c, 8);
-        if (!need(&c, kl) || kl >= sizeof m->kvs[i].key) goto bad;
-        memcpy(m->kvs[i].key, c.p + c.pos, kl);
-        c.pos += kl;
-        m->kvs[i].type = (uint32_t)rd(&c, 4);
-        if (!skip_value(&c, m->kvs[i].type, &m->kvs[i])) goto bad;
-        m->n_kv++;
+    if (!m) {
+        *msg = "out of memory";
+        return E_INTERNAL;
     }
-    uint64_t* offs = (uint64_t*)calloc(n_t ? n_t : 1, 8);
-    for (uint64_t i = 0; i < n_t; i++) {
-        uint64_t nl = rd(&c, 8);
-        if (!need(&c, nl) || nl >= sizeof m->tensors[i].name) {
-            free(offs);
-            goto bad;
-        }
-        memcpy(m->tensors[i].name, c.p + c.pos, nl);
-        c.pos += nl;
-        uint32_t nd = (uint32_t)rd(&c, 4);
-        if (nd > 8) {
-            free(offs);
-            goto bad;
-        }
-        uint64_t numel = 1;
-        for (uint32_t d = 0; d < nd; d++) numel *= rd(&c, 8);
-        m->tensors[i].numel = numel;
-        m->tensors[i].type = (uint32_t)rd(&c, 4);
-        offs[i] = rd(&c, 8);
-        if (c.bad) {
-            free(offs);
-            goto bad;
-        }
-        m->n_tensors++;
-    }
-    {
-        const kv_t* al = find_kv(m, "general.alignment");
-        uint64_t alignment = (al && al->type == T_U32) ? al->num : 32;
-        if (alignment == 0) {
-            free(offs);
-            goto bad;
-        }
-        size_t base = (size_t)((c.pos + alignment - 1) / alignment * alignment);
-        for (size_t i = 0; i < m->n_tensors; i++) {
-            int ok;
-            size_t nb = bytes_for(m->tensors[i].type, m->tensors[i].numel, &ok);
-            if (!ok || base + offs[i] + nb > len) {
-                free(offs);
-                goto bad;
-            }
-            m->tensors[i].bytes = blob + base + offs[i];
-            m->tensors[i].nbytes = nb;
-        }
-    }
-    free(offs);
-
-    {
-        /* Config::from_gguf (src/model/config.rs:156-213) */
-        const kv_t* a = find_kv(m, "general.architecture");
-        char arch[64] = {0}, key[160];
-        if (!a || a->type != T_STR || a->str_len >= sizeof arch) {
-            *msg = "gguf: missing 'general.architecture' metadata";
+    /* f32 tensors are read in place as floats: keep the blob 4-byte aligned
+     * whatever general.alignment says (numpy buffers are 16-byte aligned) */
+    if ((uintptr_t)blob & 15) {
+        m->aligned = (uint8_t*)malloc(len ? len : 1);
+        if (!m->aligned) {
             vtqo_model_free(m);
-            return 1;
+            *msg = "out of memory";
+            return E_INTERNAL;
         }
-        memcpy(arch, a->str, a->str_len);
-#define META(suffix, dst)                                          \
-    snprintf(key, sizeof key, "%s.%s", arch, suffix);              \
-    if (!read_usize(m, key, dst)) {                                \
-        *msg = "gguf: numeric metadata missing or wrong type";     \
-        vtqo_model_free(m);                                        \
-        return 1;                                                  \
+        memcpy(m->aligned, blob, len);
+        blob = m->aligned;
     }
-        META("embedding_length", &m->dim);
-        META("feed_forward_length", &m->hidden);
-        META("block_count", &m->n_layers);
-        META("attention.head_count", &m->n_heads);
-        snprintf(key, sizeof key, "%s.attention.head_count_kv", arch);
-        if (!read_usize(m, key, &m->n_kv_heads)) m->n_kv_heads = m->n_heads;
-        META("context_length", &m->seq_len);
-        const kv_t* toks = find_kv(m, "tokenizer.ggml.tokens");
-        if (toks && toks->type == T_ARR) {
-            m->vocab = (int)toks->str_len;
-        } else {
-            META("vocab_size", &m->vocab);
-        }
-#undef META
-        m->shared = find_t(m, "output.weight") == NULL;
-        snprintf(key, sizeof key, "%s.rope.freq_base", arch);
-        m->rope_theta = read_f32_meta(m, key, 10000.0f);
-        snprintf(key, sizeof key, "%s.attention.layer_norm_rms_epsilon", arch);
-        m->rms_eps = read_f32_meta(m, key, 1e-5f);
-        m->rope_neox = !strcmp(arch, "qwen2");
-    }
-    if (!get_qt(m, "token_embd.weight", &m->tok_embd) ||
-        !(m->rms_final = get_f32(m, "output_norm.weight", (size_t)m->dim))) {
-        *msg = "gguf: required Llama tensor not found";
+    int rc = gguf_parse(m, blob, len, msg);
+    if (!rc) rc = describe(m, msg);
+    if (rc) {
         vtqo_model_free(m);
-        return 1;
-    }
-    if (!m->shared) get_qt(m, "output.weight", &m->wcls);
-    m->layers = (layer_t*)calloc((size_t)m->n_layers, sizeof(layer_t));
-    for (int l = 0; l < m->n_layers; l++) {
-        char nm[96];
-        layer_t* L = &m->layers[l];
-#define QT(field, suffix)                                       \
-    snprintf(nm, sizeof nm, "blk.%d.%s", l, suffix);            \
-    if (!get_qt(m, nm, &L->field)) {                            \
-        *msg = "gguf: required Llama tensor not found";         \
-        vtqo_model_free(m);                                     \
-        return 1;                                               \
-    }
-        QT(wq, "attn_q.weight");
-        QT(wk, "attn_k.weight");
-        QT(wv, "attn_v.weight");
-        QT(wo, "attn_output.weight");
-        QT(w1, "ffn_gate.weight");
-        QT(w2, "ffn_down.weight");
-        QT(w3, "ffn_up.weight");
-#undef QT
-        snprintf(nm, sizeof nm, "blk.%d.attn_norm.weight", l);
-        L->rms_att = get_f32(m, nm, (size_t)m->dim);
-        snprintf(nm, sizeof nm, "blk.%d.ffn_norm.weight", l);
-        L->rms_ffn = get_f32(m, nm, (size_t)m->dim);
-        if (!L->rms_att || !L->rms_ffn) {
-            *msg = "gguf: expected F32 norm-weight tensor, got something else";
-            vtqo_model_free(m);
-            return 1;
-        }
-        const int kv_dim = m->n_kv_heads * (m->dim / m->n_heads);
-        snprintf(nm, sizeof nm, "blk.%d.attn_q.bias", l);
-        L->bq = get_f32(m, nm, (size_t)m->dim);
-        snprintf(nm, sizeof nm, "blk.%d.attn_k.bias", l);
-        L->bk = get_f32(m, nm, (size_t)kv_dim);
-        snprintf(nm, sizeof nm, "blk.%d.attn_v.bias", l);
-        L->bv = get_f32(m, nm, (size_t)kv_dim);
+        return rc;
     }
     *out = m;
     return 0;
-bad:
-    *msg = "gguf: malformed or truncated file";
-    vtqo_model_free(m);
-    return 1;
 }
 
 void vtqo_model_dims(const vtqo_model* m, int dims[7]) {
@@ -449,9 +645,26 @@ typedef struct {
     const char* msg;
 } run_t;
 
+/* linear_dispatch's status is the step's (1 Internal, 3 NotImplemented) */
 static int linear(run_t* r, const qt_t* w, const float* x, int in_f, int out_f, float* y) {
     return vtqo_linear_dispatch(w->dtype, r->regime, x, (size_t)in_f, w->w, w->len, y, (size_t)out_f, 1,
                                 (size_t)in_f, (size_t)out_f, out_f >= 512 ? r->threads : 1, &r->msg);
+}
+
+/* rms_norm_slice's shape check (rms_norm.rs:80-85), then the norm */
+static int norm(run_t* r, const f32v_t* w, const float* x, int n, float* out) {
+    if (w->n != (size_t)n) {
+        r->msg = "expected weight length == last dim of x, got weight mismatch";
+        return E_SHAPE_MISMATCH;
+    }
+    vtqo_rms_norm(x, w->v, n, r->m->rms_eps, out);
+    return 0;
+}
+
+/* add_bias (forward_quantized.rs:807-813): zips the two slices */
+static void add_bias(float* v, size_t n, const f32v_t* b) {
+    const size_t k = b->n < n ? b->n : n;
+    for (size_t i = 0; i < k; i++) v[i] += b->v[i];
 }
 
 /* rms_norm_slice (src/ops/rms_norm.rs:60-110) */
@@ -478,29 +691,40 @@ void vtqo_softmax(float* x, int n) {
 }
 
 /* embedding_row (src/model/forward_quantized.rs:818-923) */
-static int embedding_row(run_t* r, const qt_t* t, int row, int dim, float* out) {
-    size_t rb;
+static int embedding_row(run_t* r, const qt_t* t, uint32_t row, int dim, float* out) {
+    size_t blk, bb;
+    const char *dim_msg, *row_msg;
     int (*deq)(const uint8_t*, size_t, float*, const char**) = NULL;
     switch (t->dtype) {
     case 0:
-        if (t->len < (size_t)(row + 1) * dim * 4) {
+        if ((unsigned __int128)t->len < ((unsigned __int128)row + 1) * (unsigned)dim * 4) {
             r->msg = "embedding_row F32: table too small for token id";
-            return 1;
+            return E_INTERNAL;
         }
         memcpy(out, t->w + (size_t)row * dim * 4, (size_t)dim * 4);
         return 0;
-    case 2: rb = (size_t)dim / 32 * 18; deq = vtqo_dequantize_q4_0; break;
-    case 6: rb = (size_t)dim / 32 * 22; deq = vtqo_dequantize_q5_0; break;
-    case 8: rb = (size_t)dim / 32 * 34; deq = vtqo_dequantize_q8_0; break;
-    case 12: rb = (size_t)dim / 256 * 144; deq = vtqo_dequantize_q4_k; break;
-    case 14: rb = (size_t)dim / 256 * 210; deq = vtqo_dequantize_q6_k; break;
+    case 2: blk = 32; bb = 18; deq = vtqo_dequantize_q4_0;
+        dim_msg = "embedding_row Q4_0: dim must be a multiple of 32"; row_msg = "embedding_row Q4_0: row past end of table"; break;
+    case 12: blk = 256; bb = 144; deq = vtqo_dequantize_q4_k;
+        dim_msg = "embedding_row Q4_K: dim must be a multiple of 256"; row_msg = "embedding_row Q4_K: row past end of table"; break;
+    case 14: blk = 256; bb = 210; deq = vtqo_dequantize_q6_k;
+        dim_msg = "embedding_row Q6_K: dim must be a multiple of 256"; row_msg = "embedding_row Q6_K: row past end of table"; break;
+    case 6: blk = 32; bb = 22; deq = vtqo_dequantize_q5_0;
+        dim_msg = "embedding_row Q5_0: dim must be a multiple of 32"; row_msg = "embedding_row Q5_0: row past end of table"; break;
+    case 8: blk = 32; bb = 34; deq = vtqo_dequantize_q8_0;
+        dim_msg = "embedding_row Q8_0: dim must be a multiple of 32"; row_msg = "embedding_row Q8_0: row past end of table"; break;
     default:
         r->msg = "embedding_row: non-Q4_0 / Q4_K / Q6_K / Q8_0 / F32 embedding dtype";
-        return 1;
+        return E_NOT_IMPLEMENTED;
     }
-    if ((size_t)(row + 1) * rb > t->len) {
-        r->msg = "embedding_row: row past end of table";
-        return 1;
+    if ((size_t)dim % blk) {
+        r->msg = dim_msg;
+        return E_INTERNAL;
+    }
+    const size_t rb = (size_t)dim / blk * bb;
+    if ((unsigned __int128)((size_t)row + 1) * rb > t->len) {
+        r->msg = row_msg;
+        return E_INTERNAL;
     }
     return deq(t->w + (size_t)row * rb, rb, out, &r->msg);
 }
@@ -511,22 +735,23 @@ static int step(run_t* r, uint32_t token, int pos) {
     const int kv_mul = m->n_heads / m->n_kv_heads, hidden = m->hidden;
     rec_t* rc = r->rec;
     const uint32_t tk = (uint32_t)pos;
-    if (embedding_row(r, &m->tok_embd, (int)token, dim, r->x)) return 1;
+    int e;
+    if ((e = embedding_row(r, &m->tok_embd, token, dim, r->x))) return e;
     rec_act(rc, tk, NO_LAYER, "post_embed", r->x, dim);
     for (int l = 0; l < m->n_layers; l++) {
         const layer_t* L = &m->layers[l];
         const uint8_t(*P)[32] = rc && rc->params ? rc->params[l] : NULL;
-        vtqo_rms_norm(r->x, L->rms_att, dim, m->rms_eps, r->xb);
+        if ((e = norm(r, &L->rms_att, r->x, dim, r->xb))) return e;
         rec_op(rc, "rms_norm", (uint32_t)l, P ? P[0] : NULL, r->x, dim, r->xb, dim);
-        if (linear(r, &L->wq, r->xb, dim, m->n_heads * head, r->q)) return 1;
+        if ((e = linear(r, &L->wq, r->xb, dim, m->n_heads * head, r->q))) return e;
         rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[1] : NULL, r->xb, dim, r->q, (size_t)m->n_heads * head);
-        if (L->bq) for (int i = 0; i < dim; i++) r->q[i] += L->bq[i];
-        if (linear(r, &L->wk, r->xb, dim, kv_dim, r->k)) return 1;
+        add_bias(r->q, (size_t)dim, &L->bq);
+        if ((e = linear(r, &L->wk, r->xb, dim, kv_dim, r->k))) return e;
         rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[2] : NULL, r->xb, dim, r->k, kv_dim);
-        if (L->bk) for (int i = 0; i < kv_dim; i++) r->k[i] += L->bk[i];
-        if (linear(r, &L->wv, r->xb, dim, kv_dim, r->v)) return 1;
+        add_bias(r->k, (size_t)kv_dim, &L->bk);
+        if ((e = linear(r, &L->wv, r->xb, dim, kv_dim, r->v))) return e;
         rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[3] : NULL, r->xb, dim, r->v, kv_dim);
-        if (L->bv) for (int i = 0; i < kv_dim; i++) r->v[i] += L->bv[i];
+        add_bias(r->v, (size_t)kv_dim, &L->bv);
         const size_t loff = (size_t)l * m->seq_len * kv_dim;
         float* kc = r->key_cache + loff + (size_t)pos * kv_dim;
         memcpy(kc, r->k, (size_t)kv_dim * 4);
@@ -586,30 +811,30 @@ static int step(run_t* r, uint32_t token, int pos) {
                 for (int d = 0; d < head; d++) xo[d] += a * vt[d];
             }
         }
-        if (linear(r, &L->wo, r->xb_out, dim, dim, r->xb2)) return 1;
+        if ((e = linear(r, &L->wo, r->xb_out, dim, dim, r->xb2))) return e;
         rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[4] : NULL, r->xb_out, dim, r->xb2, dim);
         for (int i = 0; i < dim; i++) r->x[i] = r->x[i] + r->xb2[i];
         rec_act(rc, tk, (uint32_t)l, "post_attn", r->x, dim);
-        vtqo_rms_norm(r->x, L->rms_ffn, dim, m->rms_eps, r->xb);
+        if ((e = norm(r, &L->rms_ffn, r->x, dim, r->xb))) return e;
         rec_op(rc, "rms_norm", (uint32_t)l, P ? P[5] : NULL, r->x, dim, r->xb, dim);
-        if (linear(r, &L->w1, r->xb, dim, hidden, r->gate)) return 1;
+        if ((e = linear(r, &L->w1, r->xb, dim, hidden, r->gate))) return e;
         rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[6] : NULL, r->xb, dim, r->gate, hidden);
-        if (linear(r, &L->w3, r->xb, dim, hidden, r->up)) return 1;
+        if ((e = linear(r, &L->w3, r->xb, dim, hidden, r->up))) return e;
         rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[8] : NULL, r->xb, dim, r->up, hidden);
         for (int i = 0; i < hidden; i++) {
             const float g = r->gate[i];
             const float silu = g / (1.0f + vtqo_expf(-g));
             r->ffn[i] = silu * r->up[i];
         }
-        if (linear(r, &L->w2, r->ffn, hidden, dim, r->xb2)) return 1;
+        if ((e = linear(r, &L->w2, r->ffn, hidden, dim, r->xb2))) return e;
         rec_op(rc, "linear_q4_0", (uint32_t)l, P ? P[7] : NULL, r->ffn, hidden, r->xb2, dim);
         for (int i = 0; i < dim; i++) r->x[i] = r->x[i] + r->xb2[i];
         rec_act(rc, tk, (uint32_t)l, "post_ffn", r->x, dim);
     }
-    vtqo_rms_norm(r->x, m->rms_final, dim, m->rms_eps, r->xb);
+    if ((e = norm(r, &m->rms_final, r->x, dim, r->xb))) return e;
     rec_op(rc, "rms_norm", NO_LAYER, rc ? rc->rms_final : NULL, r->x, dim, r->xb, dim);
     rec_act(rc, tk, NO_LAYER, "pre_lm_head", r->xb, dim);
-    if (linear(r, m->shared ? &m->tok_embd : &m->wcls, r->xb, dim, m->vocab, r->logits)) return 1;
+    if ((e = linear(r, m->shared ? &m->tok_embd : &m->wcls, r->xb, dim, m->vocab, r->logits))) return e;
     rec_op(rc, "linear_q4_0", NO_LAYER, rc ? (m->shared ? rc->tok : rc->wcls) : NULL, r->xb, dim, r->logits,
            m->vocab);
     rec_act(rc, tk, NO_LAYER, "post_lm_head", r->logits, m->vocab);
@@ -637,16 +862,17 @@ static void le32(uint8_t* o, uint32_t v) {
 
 static int run_impl(const vtqo_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
                     const uint32_t* prompt, int prompt_len, int n_new, int threads, float* logits, uint32_t* tokens,
-                    rec_t* rec, uint8_t digest[32], const char** msg) {
-    if (prompt_len == 0) {
+                    rec_t* rec, uint8_t digest[32], uint8_t* digest_v1, const char** msg) {
+    /* inference.rs:301-311 (usize there: the sum cannot wrap) */
+    if (prompt_len <= 0) {
         *msg = "prompt_tokens must not be empty";
-        return 1;
+        return E_INVALID_SHAPE;
+    }
+    if ((int64_t)prompt_len + n_new > (int64_t)m->seq_len) {
+        *msg = "prompt + n_new_tokens exceeds seq_len";
+        return E_INVALID_SHAPE;
     }
     const int total = prompt_len + n_new;
-    if (total > m->seq_len) {
-        *msg = "prompt + n_new_tokens exceeds seq_len";
-        return 1;
-    }
     const int dim = m->dim, head = dim / m->n_heads, kv_dim = m->n_kv_heads * head;
     run_t r;
     memset(&r, 0, sizeof r);
@@ -660,6 +886,13 @@ static int run_impl(const vtqo_model* m, int regime, const char* model_id, const
     float* buf = (float*)calloc((size_t)6 * dim + 2 * (size_t)kv_dim + (size_t)m->seq_len + 3 * (size_t)m->hidden +
                                     (size_t)m->vocab,
                                 4);
+    if (!r.key_cache || !r.value_cache || !buf) {
+        free(buf);
+        free(r.key_cache);
+        free(r.value_cache);
+        *msg = "out of memory";
+        return E_INTERNAL;
+    }
     float* p = buf;
     r.x = p; p += dim;
     r.xb = p; p += dim;
@@ -710,6 +943,10 @@ static int run_impl(const vtqo_model* m, int regime, const char* model_id, const
         } else {
             vtqo_digest_v2_full(5, in_names, in_data, in_lens, 2, out_names, out_data, out_lens, rec ? rec->n_ops : 0,
                                 rec ? rec->ops : NULL, rec ? rec->n_acts : 0, rec ? rec->acts : NULL, digest);
+            if (digest_v1)
+                vtqo_digest_v1_full(5, in_names, in_data, in_lens, 2, out_names, out_data, out_lens,
+                                    rec ? rec->n_ops : 0, rec ? rec->ops : NULL, rec ? rec->n_acts : 0,
+                                    rec ? rec->acts : NULL, digest_v1);
         }
         free(pb);
         free(ob);
@@ -724,24 +961,24 @@ static int run_impl(const vtqo_model* m, int regime, const char* model_id, const
 
 int vtqo_run_quantized(const vtqo_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
                        const uint32_t* prompt, int prompt_len, int n_new, int threads, float* logits,
-                       uint32_t* tokens, uint8_t digest[32], const char** msg) {
+                       uint32_t* tokens, uint8_t digest[32], uint8_t digest_v1[32], const char** msg) {
     return run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, threads, logits, tokens, NULL,
-                    digest, msg);
+                    digest, digest_v1, msg);
 }
 
 /* PerOpRecorder::new (forward_quantized.rs:76-105): every weight hashed once */
 static void params_cache(const vtqo_model* m, rec_t* rc) {
     vtqo_blake3_hash(m->tok_embd.w, m->tok_embd.len, rc->tok);
-    hash_f32(m->rms_final, (size_t)m->dim, rc->rms_final);
+    hash_f32(m->rms_final.v, m->rms_final.n, rc->rms_final);
     if (!m->shared) vtqo_blake3_hash(m->wcls.w, m->wcls.len, rc->wcls);
     for (int l = 0; l < m->n_layers; l++) {
         const layer_t* L = &m->layers[l];
-        hash_f32(L->rms_att, (size_t)m->dim, rc->params[l][0]);
+        hash_f32(L->rms_att.v, L->rms_att.n, rc->params[l][0]);
         vtqo_blake3_hash(L->wq.w, L->wq.len, rc->params[l][1]);
         vtqo_blake3_hash(L->wk.w, L->wk.len, rc->params[l][2]);
         vtqo_blake3_hash(L->wv.w, L->wv.len, rc->params[l][3]);
         vtqo_blake3_hash(L->wo.w, L->wo.len, rc->params[l][4]);
-        hash_f32(L->rms_ffn, (size_t)m->dim, rc->params[l][5]);
+        hash_f32(L->rms_ffn.v, L->rms_ffn.n, rc->params[l][5]);
         vtqo_blake3_hash(L->w1.w, L->w1.len, rc->params[l][6]);
         vtqo_blake3_hash(L->w2.w, L->w2.len, rc->params[l][7]);
         vtqo_blake3_hash(L->w3.w, L->w3.len, rc->params[l][8]);
@@ -763,7 +1000,7 @@ int vtqo_run_quantized_recorded(const vtqo_model* m, int regime, const char* mod
     }
     if (flags & VTQO_RECORD_OPS) params_cache(m, &rc);
     const int err = run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, threads, NULL, tokens, &rc,
-                             digest, msg);
+                             digest, NULL, msg);
     if (!err) {
         if (n_ops) *n_ops = rc.n_ops;
         if (n_acts) *n_acts = rc.n_acts;

@@ -61,8 +61,16 @@ void vtqo_digest_v2(int n_in, const char *const *in_names, const uint8_t *const 
 
 /* ---- model + decode ---- */
 typedef struct vtqo_model vtqo_model;
-/* Parse a GGUF blob (borrowed; must outlive the model).  0 on success,
- * nonzero with msg set otherwise. */
+/* Status codes of the model functions, as the reference's Error variants
+ * (the numbering of include/vtq.h): 1 Internal, 3 NotImplemented,
+ * 5 Malformed, 6 Truncated, 7 Overflow, 8 ShapeMismatch, 9 InvalidShape. */
+
+/* GgufFile::parse (level 0, src/model/gguf.rs:305-421), plus
+ * Config::from_gguf and QuantizedWeights::from_gguf (level 1).  0 or the
+ * status of the first failing check, with the reference's text in msg. */
+int vtqo_gguf_parse(const uint8_t *blob, size_t len, int level, const char **msg);
+/* Parse a GGUF blob (borrowed; must outlive the model): vtqo_gguf_parse
+ * level 1.  0 on success, a status with msg set otherwise. */
 int vtqo_model_load(const uint8_t *blob, size_t len, vtqo_model **out, const char **msg);
 void vtqo_model_free(vtqo_model *m);
 /* dim, hidden, layers, heads, kv_heads, vocab, seq_len */
@@ -71,11 +79,12 @@ void vtqo_model_dims(const vtqo_model *m, int dims[7]);
 /* inference::run_quantized: regime 0 = std-parallel integer Q4_K,
  * 1 = float-fused Q4_K.  logits (may be NULL) receives
  * (prompt_len + n_new) * vocab floats, one row per decode step.
- * tokens receives n_new ids; digest the v2 model digest.  weights_hash is
- * BLAKE3 of the whole GGUF blob.  0 on success. */
+ * tokens receives n_new ids; digest the v2 model digest, digest_v1 (may be
+ * NULL) the v1 digest of the same cert.  weights_hash is BLAKE3 of the whole
+ * GGUF blob.  0 on success, a status with msg set otherwise. */
 int vtqo_run_quantized(const vtqo_model *m, int regime, const char *model_id, const uint8_t weights_hash[32],
                        const uint32_t *prompt, int prompt_len, int n_new, int threads, float *logits,
-                       uint32_t *tokens, uint8_t digest[32], const char **msg);
+                       uint32_t *tokens, uint8_t digest[32], uint8_t digest_v1[32], const char **msg);
 
 /* PerOp / activation receipts (src/model/forward_quantized.rs:64-132,
  * :260-284; src/cert/builder.rs:251-305, :489-560).  op_name is
@@ -96,6 +105,13 @@ typedef struct {
 
 /* compute_digest_v2 with op and activation sections (no interventions) */
 void vtqo_digest_v2_full(int n_in, const char *const *in_names, const uint8_t *const *in_data, const size_t *in_lens,
+                         int n_out, const char *const *out_names, const uint8_t *const *out_data,
+                         const size_t *out_lens, size_t n_ops, const vtqo_op_record *ops, size_t n_acts,
+                         const vtqo_act_record *acts, uint8_t out[32]);
+
+/* compute_digest_v1 (src/cert/builder.rs:476-487): the frozen v1 domain, no
+ * regime, the same sections */
+void vtqo_digest_v1_full(int n_in, const char *const *in_names, const uint8_t *const *in_data, const size_t *in_lens,
                          int n_out, const char *const *out_names, const uint8_t *const *out_data,
                          const size_t *out_lens, size_t n_ops, const vtqo_op_record *ops, size_t n_acts,
                          const vtqo_act_record *acts, uint8_t out[32]);

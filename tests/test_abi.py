@@ -88,7 +88,7 @@ def test_runtime_library_exports_its_header():
     exported = sorted(set(re.findall(r"\sT\s+(vtqrt_\w+)", out.stdout)))
     assert decl == exported
     lib = runtime.lib()
-    assert lib.vtqrt_run(None, 0, b"m", None, None, 1, 1, None, None, None) == vtq.E_INVALID_ARGUMENT
+    assert lib.vtqrt_run(None, 0, b"m", None, None, 1, 1, None, None, None, None) == vtq.E_INVALID_ARGUMENT
     assert b"null" in lib.vtqrt_last_error(None)
 
 

@@ -24,8 +24,8 @@ WIDE = dict(dim=2560, hidden=4352, layers=1, heads=20, kv_heads=4, vocab=512, ct
             rms_eps=1e-5)
 
 
-def compare(cfg, prompt_len, n_new, regimes=(0, 1), threads=8):
-    blob, prompt = synth.e2e_inputs(cfg, prompt_len)
+def compare(cfg, prompt_len, n_new, regimes=(0, 1), threads=8, **variant):
+    blob, prompt = synth.e2e_inputs(cfg, prompt_len, **variant)
     wh_o = bytes.fromhex(oracle.blake3(blob))
     wh_p = runtime.blake3(blob)
     assert wh_o == wh_p
@@ -40,6 +40,8 @@ def compare(cfg, prompt_len, n_new, regimes=(0, 1), threads=8):
             assert bad.size == 0, f"regime {regime}: logits differ first at step {bad[0]}"
             assert np.array_equal(t_g, t_o), f"regime {regime}: tokens {t_g} vs {t_o}"
             assert d_g == d_o, f"regime {regime}: digest {d_g} vs {d_o}"
+            # compute_digest_v1 of the same cert (vitni-receipt's model_digest_v1)
+            assert gm.digest_v1 == om.digest_v1 != d_o
     finally:
         gm.close()
     return d_o
@@ -59,16 +61,51 @@ def test_e2e_wide_long_context():
     compare(WIDE, 250, 12, regimes=(0,), threads=16)
 
 
-def test_e2e_errors_mirror_reference():
-    blob, prompt = synth.e2e_inputs(SMALL, 4)
-    gm = runtime.Model(blob)
+def test_e2e_qwen2_neox_bias_tied_head():
+    """The paths a Llama file does not take (forward_quantized.rs:389-445,
+    :617-627): qwen2.* metadata (NeoX split-half RoPE, rope base 1e6, eps
+    1e-6), q/k/v biases, the tied head (token_embd as the lm_head), and
+    general.alignment 8 (tensors off 16 bytes in the file)."""
+    cfg = dict(SMALL, rope_theta=1e6, rms_eps=1e-6)
+    compare(cfg, 6, 10, arch="qwen2", qkv_bias=True, tied=True, alignment=8)
+    compare(MEDIUM, 5, 12, regimes=(0,), arch="qwen2", qkv_bias=True)
+    compare(MEDIUM, 3, 9, regimes=(1,), tied=True, qkv_bias=True, alignment=4)
+
+
+def _errors(m, prompt, n_new, regime=0):
     try:
-        with pytest.raises(Exception, match="exceeds seq_len"):
-            gm.run(prompt, SMALL["ctx"], b"\0" * 32)
-        with pytest.raises(Exception, match="must not be empty"):
-            gm.run(np.zeros(0, dtype=np.uint32), 4, b"\0" * 32)
-    finally:
-        gm.close()
+        m.run(prompt, n_new, b"\0" * 32, regime=regime)
+    except Exception as e:  # noqa: BLE001 - both sides' exception types carry code and message
+        return (e.code, e.message)
+    return None
+
+
+def test_e2e_errors_mirror_reference():
+    import gguf_edit
+
+    cfg = dict(SMALL, vocab=256)
+    blob, prompt = synth.e2e_inputs(cfg, 4)
+    short, _ = synth.e2e_inputs(cfg, 4, short_rows=4)
+    bad_norm = gguf_edit.set_tensor_dims(blob, "blk.1.ffn_norm.weight", [252])
+    cases = [
+        (blob, prompt, cfg["ctx"], 0, (9, "prompt + n_new_tokens exceeds seq_len")),
+        (blob, np.zeros(0, dtype=np.uint32), 4, 0, (9, "prompt_tokens must not be empty")),
+        (blob, np.array([3, 256], dtype=np.uint32), 2, 0, (1, "embedding_row Q4_K: row past end of table")),
+        # a K projection 4 rows short: refused on the host before any launch
+        (short, prompt, 2, 0, (1, "linear_q4_k_integer: weight shape mismatch")),
+        (short, prompt, 2, 1, (1, "linear_q4_k_fused: weight shape mismatch")),
+        (bad_norm, prompt, 2, 0, (8, "expected weight length == last dim of x, got weight mismatch")),
+    ]
+    for b, p, n, regime, want in cases:
+        gm = runtime.Model(b)
+        try:
+            assert _errors(gm, p, n, regime) == want
+            assert _errors(oracle.Model(b), p, n, regime) == want
+            # the model still runs after a refused call
+            if b is blob:
+                gm.run(prompt, 2, b"\0" * 32)
+        finally:
+            gm.close()
     with pytest.raises(Exception, match="bad magic"):
         runtime.Model(np.frombuffer(b"GGML" + b"\0" * 60, dtype=np.uint8))
 

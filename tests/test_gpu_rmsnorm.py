@@ -17,7 +17,9 @@ from vtq import runtime
 
 pytestmark = pytest.mark.gpu
 
-SIZES = [1, 7, 256, 575, 576, 1000, 2048, 2049, 2560, 4096, 4607, 4608, 4609, 5000, 8192]
+# up to 32768, the entry point's limit; past 16384 the products take more
+# than 64 KiB of LDS (the kernel's raised dynamic-LDS limit)
+SIZES = [1, 7, 256, 575, 576, 1000, 2048, 2049, 2560, 4096, 4607, 4608, 4609, 5000, 8192, 16384, 16385, 32768]
 
 
 def make_x(kind, n, rng):
@@ -93,3 +95,15 @@ def test_rms_norm_many_gaussian_rows():
         x = (rng.standard_normal(2048) * rng.choice([0.01, 1.0, 30.0])).astype(np.float32)
         w = rng.standard_normal(2048).astype(np.float32)
         assert same(run_gpu(x, w, eps), oracle.rms_norm(x, w, eps))
+
+
+@pytest.mark.parametrize("n", [0, 32769])
+def test_rms_norm_rejects_sizes_outside_the_kernel(n):
+    """n = 0 and n > 32768 are refused on the host (VTQ_E_NOT_IMPLEMENTED)
+    before any launch."""
+    x = torch.zeros(max(n, 1), dtype=torch.float32, device="cuda:0")
+    y = torch.full_like(x, 7.0)
+    rc = runtime.lib().vtqrt_rms_norm_device(x.data_ptr(), x.data_ptr(), n, 1e-5, y.data_ptr(), None)
+    torch.cuda.synchronize()
+    assert rc == 3
+    assert bool((y == 7.0).all())

@@ -153,3 +153,103 @@ def test_per_op_and_activation_receipts():
     assert acts_none == [] and len(ops_only) == len(ops) and d_ops not in (d1, digest)
     _, d0, _, _ = m.run_recorded(prompt, 3, wh, flags=0)
     assert d0 == digest
+
+
+def _leb128(v):
+    out = bytearray()
+    while True:
+        b = v & 0x7F
+        v >>= 7
+        out.append(b | (0x80 if v else 0))
+        if not v:
+            return bytes(out)
+
+
+def _frame(domain, regime, inputs, outputs):
+    """write_sections (src/cert/builder.rs:491-519) with the v1 or v2 domain,
+    framed here in Python, independently of the oracle's C framing."""
+    b = bytearray(domain)
+    if regime is not None:
+        b += _leb128(len(regime)) + regime
+    for fields in (inputs, outputs):
+        b += _leb128(len(fields))
+        for k, v in fields:
+            b += _leb128(len(k)) + k.encode() + _leb128(len(v)) + v
+    b += b"\0\0\0"  # no ops, activations, interventions
+    return bytes(b)
+
+
+def test_digest_v1_is_the_frozen_framing():
+    """compute_digest_v1 (builder.rs:476-487): the v2 sections under the v1
+    domain with no regime.  The Python framing is pinned first by
+    reproducing the reference's v2 constant; under the v1 domain it must
+    then equal the oracle's v1, and v1 must differ from v2 (builder.rs:738-740)."""
+    ins = [("model_id", b"tinyllama"), ("prompt_tokens", bytes([1, 0, 0, 0]))]
+    outs = [("output_tokens", bytes([9, 0, 0, 0]))]
+    v2 = oracle.blake3(_frame(b"vitnify-receipt v2\0", b"vitni-regime-1", ins, outs))
+    assert v2 == "6d5f534cf69c441ba2832c6e63747a7989ccb5de9a2cc9dc528e5b8e0359cf1e"
+    v1 = oracle.blake3(_frame(b"vitnify-receipt v1\0", None, ins, outs))
+    assert oracle.digest_v1(ins, outs) == v1 != v2
+
+
+def test_run_quantized_v1_digest():
+    blob, prompt = synth.e2e_inputs(SMALL, 5)
+    wh = bytes.fromhex(oracle.blake3(blob))
+    m = oracle.Model(blob)
+    toks, d2, _ = m.run(prompt, 4, wh, regime=0, want_logits=False)
+    arch = (f"llama2c:dim=256,hidden=512,layers=2,heads=4,kv_heads=2,vocab=1000,seq=64,shared=false").encode()
+    ins = [("model_id", b"vitni-receipt"), ("weights_hash", wh), ("arch_hash", bytes.fromhex(oracle.blake3(arch))),
+           ("prompt_tokens", prompt.astype("<u4").tobytes()), ("n_new_tokens", (4).to_bytes(4, "little"))]
+    ob = toks.astype("<u4").tobytes()
+    outs = [("output_tokens", ob), ("output_tokens_hash", bytes.fromhex(oracle.blake3(ob)))]
+    assert d2 == oracle.blake3(_frame(b"vitnify-receipt v2\0", b"vitni-regime-1", ins, outs))
+    assert m.digest_v1 == oracle.blake3(_frame(b"vitnify-receipt v1\0", None, ins, outs)) != d2
+
+
+def test_model_variants_load():
+    """The Qwen2 layout (qwen2.* keys: NeoX RoPE), the tied head (no
+    output.weight) and attention biases parse as QuantizedWeights does, and
+    each changes the computation."""
+    cfg = dict(SMALL, vocab=256)
+    runs = {}
+    for name, kw in [("llama", {}), ("qwen2", dict(arch="qwen2")), ("tied", dict(tied=True)),
+                     ("bias", dict(qkv_bias=True)), ("align8", dict(alignment=8))]:
+        blob, prompt = synth.e2e_inputs(cfg, 6, **kw)
+        m = oracle.Model(blob)
+        assert (m.dim, m.vocab) == (256, 256)
+        t, d, lg = m.run(prompt, 4, b"\0" * 32, regime=0)
+        assert np.isfinite(lg).all()
+        runs[name] = lg
+    # alignment only moves bytes; every other variant changes the logits
+    assert np.array_equal(runs["align8"].view(np.uint32), runs["llama"].view(np.uint32))
+    for name in ("qwen2", "tied", "bias"):
+        assert not np.array_equal(runs[name], runs["llama"]), name
+
+
+def test_run_errors_follow_the_reference_order():
+    import gguf_edit
+
+    cfg = dict(SMALL, vocab=256)
+    # a K projection 4 rows short: linear_dispatch's shape check, per regime's function
+    blob, prompt = synth.e2e_inputs(cfg, 4, short_rows=4)
+    m = oracle.Model(blob)
+    with pytest.raises(oracle.OracleError) as e:
+        m.run(prompt, 2, b"\0" * 32, regime=0)
+    assert (e.value.code, e.value.message) == (1, "linear_q4_k_integer: weight shape mismatch")
+    with pytest.raises(oracle.OracleError) as e:
+        m.run(prompt, 2, b"\0" * 32, regime=1)
+    assert (e.value.code, e.value.message) == (1, "linear_q4_k_fused: weight shape mismatch")
+    # a norm weight of the wrong length: rms_norm_slice's ShapeMismatch
+    blob, prompt = synth.e2e_inputs(cfg, 4)
+    bad = gguf_edit.set_tensor_dims(blob, "blk.1.ffn_norm.weight", [252])
+    with pytest.raises(oracle.OracleError) as e:
+        oracle.Model(bad).run(prompt, 2, b"\0" * 32)
+    assert (e.value.code, e.value.message) == (8, "expected weight length == last dim of x, got weight mismatch")
+    # a prompt token past the embedding table
+    m = oracle.Model(blob)
+    with pytest.raises(oracle.OracleError) as e:
+        m.run(np.array([3, 256], dtype=np.uint32), 2, b"\0" * 32)
+    assert (e.value.code, e.value.message) == (1, "embedding_row Q4_K: row past end of table")
+    with pytest.raises(oracle.OracleError) as e:
+        m.run(np.zeros(0, dtype=np.uint32), 2, b"\0" * 32)
+    assert (e.value.code, e.value.message) == (9, "prompt_tokens must not be empty")

@@ -709,9 +709,7 @@ __global__ __launch_bounds__(kNW * 64) void kquant_windows_kernel(const float* _
 // Dynamic LDS above 64 KiB must be allowed per kernel; gfx950 has 160 KiB per CU.
 template <class K>
 static hipError_t allow_lds(K kernel, size_t bytes) {
-    if (bytes <= 65536) return hipSuccess;
-    return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                               (int)bytes);
+    return allow_dynamic_lds(reinterpret_cast<const void*>(kernel), bytes);
 }
 
 template <class K, class... A>

@@ -9,9 +9,11 @@
 #include <climits>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <utility>
 
 #include "../../include/vtq.h"
 #include "vtq_kernels.h"
@@ -291,6 +293,24 @@ int linear_host(vtq_ctx* c, int type, int regime, const float* x, size_t x_len, 
 }
 
 }  // namespace
+
+namespace vtq {
+
+hipError_t allow_dynamic_lds(const void* kernel, size_t bytes) {
+    if (bytes <= 65536) return hipSuccess;
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, size_t> raised;  // (device, kernel) -> limit set
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev)) return e;
+    std::lock_guard<std::mutex> lock(mu);
+    size_t& have = raised[{dev, kernel}];
+    if (have >= bytes) return hipSuccess;
+    if (hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)) return e;
+    have = bytes;
+    return hipSuccess;
+}
+
+}  // namespace vtq
 
 extern "C" {
 

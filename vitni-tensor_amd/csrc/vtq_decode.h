@@ -48,6 +48,10 @@ struct AttnArgs {
 };
 // RoPE of q and of this step's k, the cache write of k and v at *pos, and
 // per-head softmax attention (src/model/forward_quantized.rs:405-560).
+// attention_supported: whether the kernel takes this head dimension (a
+// multiple of 4 up to 256 that divides 16384) and cache length (its scores
+// fit in LDS beside the tiles).
+bool attention_supported(int head_dim, int seq);
 hipError_t attention(const AttnArgs& a, hipStream_t stream);
 
 // The embedding table, for the next step's row (see embed).
@@ -74,6 +78,10 @@ hipError_t argmax_advance(const float* logits, int vocab, uint32_t* tokens, int*
 // x[i] = x[i] + y[i] (residual), v[i] = v[i] + b[i] (bias),
 // out[i] = silu(gate[i]) * up[i] with silu(g) = g / (1 + expf(-g)).
 hipError_t add_inplace(float* x, const float* y, int n, hipStream_t stream);
+
+// y[7i + k] = f_k(x[i]) for the seven functions of the reference's
+// transcendental sweep, evaluated by the device libm the step uses.
+hipError_t transcendentals(const float* x, int n, float* y, hipStream_t stream);
 hipError_t swiglu(const float* gate, const float* up, float* out, int n, hipStream_t stream);
 
 }  // namespace decode

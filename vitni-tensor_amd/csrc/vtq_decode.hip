@@ -11,6 +11,7 @@
 // round exactly as the reference's libm crate does.
 #include "vtq_decode.h"
 #include "vtq_device.h"
+#include "vtq_kernels.h"
 #include "vtq_libm.h"
 
 namespace vtq {
@@ -472,29 +473,30 @@ hipError_t embed(int ggml_type, const uint8_t* table, uint32_t rows, const uint3
 
 hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out, hipStream_t stream) {
     const size_t lds = (size_t)((n + 3) & ~3) * 4;  // the serial sum reads whole float4s
-    if (lds > 65536) {
-        if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(rms_norm_kernel),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds))
-            return e;
-    }
+    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(rms_norm_kernel), lds)) return e;
     hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(256), lds, stream, x, w, n, eps, out);
     return hipGetLastError();
 }
 
 template <int HD>
 static hipError_t launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
-    if (lds > 65536) {
-        if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(attention_kernel<HD>),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds))
-            return e;
-    }
+    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(attention_kernel<HD>), lds)) return e;
     hipLaunchKernelGGL(attention_kernel<HD>, dim3((unsigned)a.heads), dim3(kAttnThreads), lds, stream, a);
     return hipGetLastError();
 }
 
+static size_t attention_lds(int head_dim, int seq) {
+    return ((size_t)3 * head_dim + kAttnThreads + 4 + (((size_t)seq + 3) & ~(size_t)3) + kAttnTile * 64) * 4;
+}
+
+bool attention_supported(int head_dim, int seq) {
+    return head_dim > 0 && head_dim <= kAttnThreads && head_dim % 4 == 0 && (kAttnTile * 64) % head_dim == 0 &&
+           seq > 0 && attention_lds(head_dim, seq) <= 160 * 1024;
+}
+
 hipError_t attention(const AttnArgs& a, hipStream_t stream) {
-    if (a.head_dim > kAttnThreads || a.head_dim % 4 || (kAttnTile * 64) % a.head_dim) return hipErrorInvalidValue;
-    const size_t lds = ((size_t)3 * a.head_dim + kAttnThreads + 4 + ((a.seq + 3) & ~3) + kAttnTile * 64) * 4;
+    if (!attention_supported(a.head_dim, a.seq)) return hipErrorInvalidValue;
+    const size_t lds = attention_lds(a.head_dim, a.seq);
     if (a.head_dim == 64) return launch_attention<64>(a, lds, stream);
     if (a.head_dim == 128) return launch_attention<128>(a, lds, stream);
     return launch_attention<0>(a, lds, stream);
@@ -504,6 +506,31 @@ hipError_t argmax_advance(const float* logits, int vocab, uint32_t* tokens, int*
                           float* hist, const EmbedArgs& e, hipStream_t stream) {
     hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(kArgThreads), 0, stream, logits, vocab, tokens, pos, prompt_len,
                        total, hist, e);
+    return hipGetLastError();
+}
+
+// The device libm of the decode step over an input array, in the order of
+// the reference's transcendental sweep (tests/transcendental_determinism.rs:
+// 34-42): expf, sqrtf(|x|), cosf, sinf, powf(1e4, x/64), powf(1e6, x/64),
+// 1 / (1 + expf(-x)).
+__global__ __launch_bounds__(256) void transcendentals_kernel(const float* __restrict__ x, int n,
+                                                             float* __restrict__ y) {
+    const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i >= n) return;
+    const float v = x[i];
+    float* o = y + (size_t)7 * i;
+    o[0] = libm::expf(v);
+    o[1] = libm::sqrtf(libm::fabsf_(v));
+    o[2] = libm::cosf(v);
+    o[3] = libm::sinf(v);
+    o[4] = libm::powf(10000.0f, v / 64.0f);
+    o[5] = libm::powf(1000000.0f, v / 64.0f);
+    o[6] = 1.0f / (1.0f + libm::expf(-v));
+}
+
+hipError_t transcendentals(const float* x, int n, float* y, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(transcendentals_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, x, n, y);
     return hipGetLastError();
 }
 

@@ -42,6 +42,11 @@ hipError_t launch_kquant_fused(int ggml_type, int epi, const float* x, const Row
 
 hipError_t launch_fill(float* y, size_t n, float v, hipStream_t stream);
 
+// Raise `kernel`'s dynamic-LDS limit to at least `bytes` on the current
+// device (gfx950 has 160 KiB per CU; the default limit is 64 KiB).  The
+// attribute is set once per (device, kernel) and size, not per launch.
+hipError_t allow_dynamic_lds(const void* kernel, size_t bytes);
+
 // Prefill GEMM (batch >= kGemmMinBatch): activation pre-pass into `workspace`
 // (q4k_gemm_workspace_bytes) followed by the i8-MFMA kernel.
 constexpr int kGemmMinBatch = 32;

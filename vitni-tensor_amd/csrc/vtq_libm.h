@@ -7,6 +7,42 @@
 // these are restatements of those published algorithms, usable from host
 // and device code.  Every operation is a separately rounded IEEE operation
 // (the library is compiled with -ffp-contract=off).
+//
+// Upstream notices.  The algorithms and their constants come from FreeBSD
+// msun by way of musl and the Rust `libm` crate, which carry these grants:
+//
+//   FreeBSD msun (e_expf.c, e_powf.c, s_sinf.c, s_cosf.c, k_sinf.c,
+//   k_cosf.c, e_rem_pio2f.c, k_rem_pio2.c):
+//     Copyright (C) 1993 by Sun Microsystems, Inc. All rights reserved.
+//     Developed at SunPro, a Sun Microsystems, Inc. business.
+//     Permission to use, copy, modify, and distribute this
+//     software is freely granted, provided that this notice
+//     is preserved.
+//   (The float versions: conversion to float by Ian Lance Taylor, Cygnus
+//   Support; optimisations by Bruce D. Evans.)
+//
+//   musl libc (the restructured expf and scalbnf), MIT licence:
+//     Copyright (c) 2005-2020 Rich Felker, et al.
+//     Permission is hereby granted, free of charge, to any person obtaining
+//     a copy of this software and associated documentation files (the
+//     "Software"), to deal in the Software without restriction, including
+//     without limitation the rights to use, copy, modify, merge, publish,
+//     distribute, sublicense, and/or sell copies of the Software, and to
+//     permit persons to whom the Software is furnished to do so, subject to
+//     the following conditions:
+//     The above copyright notice and this permission notice shall be
+//     included in all copies or substantial portions of the Software.
+//     THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND,
+//     EXPRESS OR IMPLIED, INCLUDING BUT NOT LIMITED TO THE WARRANTIES OF
+//     MERCHANTABILITY, FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT.
+//     IN NO EVENT SHALL THE AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY
+//     CLAIM, DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION OF CONTRACT,
+//     TORT OR OTHERWISE, ARISING FROM, OUT OF OR IN CONNECTION WITH THE
+//     SOFTWARE OR THE USE OR OTHER DEALINGS IN THE SOFTWARE.
+//
+//   The Rust `libm` crate (the port the reference calls) is distributed
+//   under the MIT licence above (Copyright (c) 2018 Jorge Aparicio) or
+//   Apache-2.0.
 #pragma once
 
 #include <hip/hip_runtime.h>

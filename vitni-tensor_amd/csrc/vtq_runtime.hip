@@ -37,6 +37,7 @@
 #include "../../include/vtq.h"
 #include "../../include/vtq_runtime.h"
 #include "vtq_decode.h"
+#include "vtq_gguf.h"
 #include "vtq_kernels.h"
 
 namespace {
@@ -170,100 +171,26 @@ void leb128(Blake3& h, uint64_t v) {
     h.update(b, (size_t)n);
 }
 
-// ---------------------------------------------------------------- GGUF
-struct Tensor {
-    uint32_t type = 0;
-    uint64_t numel = 0;
-    size_t offset = 0, nbytes = 0;  // within the blob
-};
-
-struct Meta {
-    uint32_t type = 0;
-    uint64_t num = 0;
-    std::string str;
-    uint64_t count = 0;  // array length
-};
-
-class Reader {
-  public:
-    Reader(const uint8_t* p, size_t n) : p_(p), n_(n) {}
-    bool ok() const { return ok_; }
-    size_t pos() const { return pos_; }
-    uint64_t uint(int bytes) {
-        if (!ok_ || n_ - pos_ < (size_t)bytes) return fail();
-        uint64_t v = 0;
-        for (int i = 0; i < bytes; i++) v |= (uint64_t)p_[pos_ + i] << (8 * i);
-        pos_ += bytes;
-        return v;
-    }
-    std::string str() {
-        const uint64_t len = uint(8);
-        if (!ok_ || n_ - pos_ < len) {
-            fail();
-            return {};
-        }
-        std::string s(reinterpret_cast<const char*>(p_ + pos_), len);
-        pos_ += len;
-        return s;
-    }
-    bool value(uint32_t t, Meta* m) {
-        static const int kSize[13] = {1, 1, 2, 2, 4, 4, 4, 1, 0, 0, 8, 8, 8};
-        if (t == 8) {
-            std::string s = str();
-            if (m) m->str = s;
-        } else if (t == 9) {
-            const uint32_t et = (uint32_t)uint(4);
-            const uint64_t n = uint(8);
-            if (m) m->count = n;
-            for (uint64_t i = 0; i < n && ok_; i++) value(et, nullptr);
-        } else if (t < 13) {
-            const uint64_t v = uint(kSize[t]);
-            if (m) m->num = v;
-        } else {
-            fail();
-        }
-        return ok_;
-    }
-
-  private:
-    uint64_t fail() {
-        ok_ = false;
-        return 0;
-    }
-    const uint8_t* p_;
-    size_t n_, pos_ = 0;
-    bool ok_ = true;
-};
-
-bool tensor_bytes(uint32_t type, uint64_t numel, size_t* out) {
-    switch (type) {
-    case 0: *out = numel * 4; return true;
-    case 1: *out = numel * 2; return true;
-    case 2: if (numel % 32) return false; *out = numel / 32 * 18; return true;
-    case 6: if (numel % 32) return false; *out = numel / 32 * 22; return true;
-    case 8: if (numel % 32) return false; *out = numel / 32 * 34; return true;
-    case 12: if (numel % 256) return false; *out = numel / 256 * 144; return true;
-    case 14: if (numel % 256) return false; *out = numel / 256 * 210; return true;
-    }
-    return false;
-}
-
-// exact f16 -> f32 (src/ops/quant.rs:40-66)
+// ---------------------------------------------------------------- model
+// A tensor as the step uses it: its bytes in the host copy of the blob (the
+// op receipts hash weights there) and its copy in the device arena.  Every
+// device copy starts 256-byte aligned, whatever general.alignment the file
+// declares.
 struct Lin {
-    int type = 0;
-    size_t offset = 0, nbytes = 0;
+    int type = -1;               // -1: absent (optional biases)
+    size_t host = 0, nbytes = 0;  // byte range in the host blob
+    size_t dev = 0;              // offset in the device arena
 };
 
 struct Layer {
-    size_t rms_att = 0, rms_ffn = 0, bq = 0, bk = 0, bv = 0;  // blob offsets of F32 tensors (0: absent)
-    Lin wq, wk, wv, wo, w1, w2, w3;
+    Lin rms_att, rms_ffn, bq, bk, bv, wq, wk, wv, wo, w1, w2, w3;
 };
 
 }  // namespace
 
 struct vtqrt_model {
-    std::vector<uint8_t> blob;  // host copy (metadata, shapes)
-    uint8_t* dblob = nullptr;   // device copy: every tensor is read in place
+    std::vector<uint8_t> blob;  // host copy (the op receipts hash the weights there)
+    uint8_t* dblob = nullptr;   // device arena: one aligned copy of every tensor the step reads
     vtq_ctx* ctx = nullptr;
     hipStream_t stream = nullptr;
     std::string err;
@@ -271,8 +198,7 @@ struct vtqrt_model {
     int dim = 0, hidden = 0, layers = 0, heads = 0, kv_heads = 0, vocab = 0, seq = 0;
     bool shared = false, neox = false;
     float theta = 10000.0f, eps = 1e-5f;
-    Lin tok, wcls;
-    size_t rms_final = 0;  // blob offsets of F32 tensors
+    Lin tok, wcls, rms_final;
     std::vector<Layer> L;
     // device state of a run: activations, KV cache, tokens, position
     float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr, *gate = nullptr,
@@ -302,13 +228,13 @@ int hip_check(vtqrt_model* m, hipError_t e, const char* where) {
     return fail(m, VTQ_E_GPU, std::string("GpuError: ") + where + ": " + hipGetErrorString(e));
 }
 
-const float* f32_at(const vtqrt_model* m, size_t off) {
-    return off ? reinterpret_cast<const float*>(m->dblob + off) : nullptr;
+const float* f32_at(const vtqrt_model* m, const Lin& t) {
+    return t.type >= 0 ? reinterpret_cast<const float*>(m->dblob + t.dev) : nullptr;
 }
 
 // y = W x through the C ABI (any type, either regime)
 int linear(vtqrt_model* m, int regime, const Lin& w, const float* x, int in_feat, int out_feat, float* y) {
-    const int rc = vtq_linear_device(m->ctx, w.type, regime, x, m->dblob + w.offset, w.nbytes, y, 1, (size_t)in_feat,
+    const int rc = vtq_linear_device(m->ctx, w.type, regime, x, m->dblob + w.dev, w.nbytes, y, 1, (size_t)in_feat,
                                      (size_t)out_feat, m->stream);
     return rc ? fail(m, rc, vtq_last_error(m->ctx)) : VTQ_OK;
 }
@@ -323,14 +249,14 @@ uint32_t table_rows(const vtqrt_model* m) {
 // integer regime or Q6_K (always integer, linear_dispatch arm Q6_K), and the
 // shapes fit the rows kernel.
 bool fused_args(const vtqrt_model* m, int regime, int epi, std::initializer_list<const Lin*> ws,
-                std::initializer_list<int> rows, size_t norm_off, int in_feat, vtq::RowsArgs* a, int* type) {
-    *a = vtq::RowsArgs{{nullptr, nullptr, nullptr}, {0, 0, 0}, f32_at(m, norm_off), m->eps};
+                std::initializer_list<int> rows, const Lin* norm, int in_feat, vtq::RowsArgs* a, int* type) {
+    *a = vtq::RowsArgs{{nullptr, nullptr, nullptr}, {0, 0, 0}, norm ? f32_at(m, *norm) : nullptr, m->eps};
     *type = -1;
     int i = 0;
     for (const Lin* w : ws) {
         if ((*type >= 0 && w->type != *type) || !(w->type == 14 || (w->type == 12 && regime == 0))) return false;
         *type = w->type;
-        a->w[i++] = m->dblob + w->offset;
+        a->w[i++] = m->dblob + w->dev;
     }
     i = 0;
     for (int r : rows) a->rows[i++] = r;
@@ -344,8 +270,8 @@ int launch_fused(vtqrt_model* m, int type, int epi, const float* x, const vtq::R
 }
 
 // rms_norm(x, w) into xb for linears that do not normalise in their own prologue
-int norm_to_xb(vtqrt_model* m, size_t w_off) {
-    return hip_check(m, vtq::decode::rms_norm(m->x, f32_at(m, w_off), m->dim, m->eps, m->xb, m->stream), "rms_norm");
+int norm_to_xb(vtqrt_model* m, const Lin& w) {
+    return hip_check(m, vtq::decode::rms_norm(m->x, f32_at(m, w), m->dim, m->eps, m->xb, m->stream), "rms_norm");
 }
 
 vtq::decode::RopeArgs rope_args(vtqrt_model* m) {
@@ -353,7 +279,7 @@ vtq::decode::RopeArgs rope_args(vtqrt_model* m) {
 }
 
 vtq::decode::EmbedArgs embed_args(vtqrt_model* m) {
-    return vtq::decode::EmbedArgs{m->tok.type, m->dblob + m->tok.offset, table_rows(m),
+    return vtq::decode::EmbedArgs{m->tok.type, m->dblob + m->tok.dev, table_rows(m),
                                   vtq::decode::embed_row_bytes(m->tok.type, m->dim), m->dim, m->x, rope_args(m)};
 }
 
@@ -368,7 +294,7 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
     for (int l = 0; !rc && l < m->layers; l++) {
         const Layer& Ly = m->L[l];
         // q | k | v = W (rms_norm(x, attn_norm))
-        if (fused_args(m, regime, vtq::kEpiStore, {&Ly.wq, &Ly.wk, &Ly.wv}, {dim, kv_dim, kv_dim}, Ly.rms_att, dim, &fa,
+        if (fused_args(m, regime, vtq::kEpiStore, {&Ly.wq, &Ly.wk, &Ly.wv}, {dim, kv_dim, kv_dim}, &Ly.rms_att, dim, &fa,
                        &type)) {
             rc = launch_fused(m, type, vtq::kEpiStore, m->x, fa, dim, m->qkv);
         } else {
@@ -396,7 +322,7 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
         a.neox = m->neox ? 1 : 0;
         if ((rc = hip_check(m, dec::attention(a, m->stream), "attention"))) break;
         // x = x + Wo att
-        if (fused_args(m, regime, vtq::kEpiAccumulate, {&Ly.wo}, {dim}, 0, dim, &fa, &type)) {
+        if (fused_args(m, regime, vtq::kEpiAccumulate, {&Ly.wo}, {dim}, nullptr, dim, &fa, &type)) {
             rc = launch_fused(m, type, vtq::kEpiAccumulate, m->att, fa, dim, m->x);
         } else {
             rc = linear(m, regime, Ly.wo, m->att, dim, dim, m->tmp);
@@ -404,7 +330,7 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
         }
         if (rc) break;
         // ffn = silu(W1 h) * (W3 h), h = rms_norm(x, ffn_norm)
-        if (fused_args(m, regime, vtq::kEpiSwiGLU, {&Ly.w1, &Ly.w3}, {hidden, hidden}, Ly.rms_ffn, dim, &fa, &type)) {
+        if (fused_args(m, regime, vtq::kEpiSwiGLU, {&Ly.w1, &Ly.w3}, {hidden, hidden}, &Ly.rms_ffn, dim, &fa, &type)) {
             rc = launch_fused(m, type, vtq::kEpiSwiGLU, m->x, fa, dim, m->ffn);
         } else {
             rc = norm_to_xb(m, Ly.rms_ffn);
@@ -414,7 +340,7 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
         }
         if (rc) break;
         // x = x + W2 ffn
-        if (fused_args(m, regime, vtq::kEpiAccumulate, {&Ly.w2}, {dim}, 0, hidden, &fa, &type)) {
+        if (fused_args(m, regime, vtq::kEpiAccumulate, {&Ly.w2}, {dim}, nullptr, hidden, &fa, &type)) {
             rc = launch_fused(m, type, vtq::kEpiAccumulate, m->ffn, fa, hidden, m->x);
         } else {
             rc = linear(m, regime, Ly.w2, m->ffn, hidden, dim, m->tmp);
@@ -424,7 +350,7 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
     if (rc) return rc;
     // logits = W_out (rms_norm(x, output_norm))
     const Lin& head_w = m->shared ? m->tok : m->wcls;
-    if (fused_args(m, regime, vtq::kEpiStore, {&head_w}, {m->vocab}, m->rms_final, dim, &fa, &type)) {
+    if (fused_args(m, regime, vtq::kEpiStore, {&head_w}, {m->vocab}, &m->rms_final, dim, &fa, &type)) {
         rc = launch_fused(m, type, vtq::kEpiStore, m->x, fa, dim, m->logits);
     } else {
         rc = norm_to_xb(m, m->rms_final);
@@ -555,8 +481,9 @@ void build_params(vtqrt_model* m) {
     if (m->params_ready) return;
     const uint8_t* b = m->blob.data();
     m->params.assign((size_t)m->layers * 9, {});
-    auto lin_hash = [&](const Lin& w, uint8_t* out) { vtqrt_blake3(b + w.offset, w.nbytes, out); };
-    auto f32_hash = [&](size_t off, uint8_t* out) { vtqrt_blake3(b + off, (size_t)m->dim * 4, out); };
+    // hash_f32_slice of a norm is BLAKE3 of its little-endian bytes: the same bytes
+    auto lin_hash = [&](const Lin& w, uint8_t* out) { vtqrt_blake3(b + w.host, w.nbytes, out); };
+    auto f32_hash = lin_hash;
     parallel_for(m->layers * 9 + 3, [&](int i) {
         if (i == m->layers * 9) return lin_hash(m->tok, m->tok_hash);
         if (i == m->layers * 9 + 1) return f32_hash(m->rms_final, m->rms_final_hash);
@@ -652,28 +579,6 @@ void record_step(vtqrt_model* m, Recorder& rec, const float* H, uint32_t token) 
     act(kNoLayer, "post_lm_head", logits);
 }
 
-const Meta* meta(const std::map<std::string, Meta>& kv, const std::string& k) {
-    auto it = kv.find(k);
-    return it == kv.end() ? nullptr : &it->second;
-}
-
-bool read_usize(const std::map<std::string, Meta>& kv, const std::string& k, int* out) {
-    const Meta* v = meta(kv, k);
-    if (!v) return false;
-    switch (v->type) {
-    case 4: case 10: *out = (int)v->num; return true;
-    case 5: if ((int32_t)v->num < 0) return false; *out = (int32_t)v->num; return true;
-    case 11: if ((int64_t)v->num < 0) return false; *out = (int)(int64_t)v->num; return true;
-    }
-    return false;
-}
-
-float read_f32(const std::map<std::string, Meta>& kv, const std::string& k, float def) {
-    const Meta* v = meta(kv, k);
-    if (!v || v->type != 6) return def;
-    return __builtin_bit_cast(float, (uint32_t)v->num);
-}
-
 }  // namespace
 
 extern "C" {
@@ -701,6 +606,14 @@ int vtqrt_rms_norm_device(const float* d_x, const float* d_w, size_t n, float ep
                : VTQ_E_GPU;
 }
 
+int vtqrt_transcendentals_device(const float* d_x, size_t n, float* d_y, void* stream) {
+    if (n && (!d_x || !d_y)) return VTQ_E_INVALID_ARGUMENT;
+    if (n > (size_t)INT32_MAX / 7) return VTQ_E_NOT_IMPLEMENTED;
+    return vtq::decode::transcendentals(d_x, (int)n, d_y, static_cast<hipStream_t>(stream)) == hipSuccess
+               ? VTQ_OK
+               : VTQ_E_GPU;
+}
+
 void vtqrt_free(vtqrt_model* m) {
     if (!m) return;
     if (m->stream) (void)hipStreamSynchronize(m->stream);
@@ -715,163 +628,132 @@ void vtqrt_free(vtqrt_model* m) {
     delete m;
 }
 
+int vtqrt_parse(const uint8_t* gguf, size_t len, int level, int dims[7], char* err, size_t err_cap) {
+    if ((!gguf && len) || level < 0 || level > 1) return VTQ_E_INVALID_ARGUMENT;
+    static const uint8_t kEmpty[1] = {0};
+    vtq::gguf::File f;
+    vtq::gguf::Model md;
+    const char* msg = "";
+    int rc = vtq::gguf::parse(gguf ? gguf : kEmpty, len, &f, &msg);
+    if (!rc && level == 1) rc = vtq::gguf::describe(f, &md, &msg);
+    if (!rc && level == 1 && dims) {
+        const int d[7] = {md.dim, md.hidden, md.layers, md.heads, md.kv_heads, md.vocab, md.seq};
+        std::memcpy(dims, d, sizeof d);
+    }
+    if (err && err_cap) {
+        std::strncpy(err, msg, err_cap - 1);
+        err[err_cap - 1] = 0;
+    }
+    return rc;
+}
+
 int vtqrt_load(int device, const uint8_t* gguf, size_t len, vtqrt_model** out) {
     if (!out || (!gguf && len)) return VTQ_E_INVALID_ARGUMENT;
     *out = nullptr;
-    auto* m = new vtqrt_model();
-    m->blob.assign(gguf, gguf + len);
-    Reader r(m->blob.data(), len);
-    if (len < 4 || std::memcmp(gguf, "GGUF", 4)) {
-        int rc = fail(m, VTQ_E_INTERNAL, "gguf: bad magic (not 'GGUF')");
-        *out = m;
-        return rc;
-    }
-    r.uint(4);
-    const uint32_t version = (uint32_t)r.uint(4);
-    const uint64_t n_t = r.uint(8), n_kv = r.uint(8);
-    std::map<std::string, Meta> kv;
-    std::map<std::string, Tensor> ts;
-    std::vector<std::pair<std::string, uint64_t>> offsets;
-    if (version != 2 && version != 3) {
-        *out = m;
-        return fail(m, VTQ_E_INTERNAL, "gguf: unsupported version (only v2/v3 supported)");
-    }
-    for (uint64_t i = 0; i < n_kv && r.ok(); i++) {
-        std::string key = r.str();
-        Meta v;
-        v.type = (uint32_t)r.uint(4);
-        if (!r.value(v.type, &v)) break;
-        kv[key] = v;
-    }
-    for (uint64_t i = 0; i < n_t && r.ok(); i++) {
-        std::string name = r.str();
-        const uint32_t nd = (uint32_t)r.uint(4);
-        if (nd > 8) {
-            *out = m;
-            return fail(m, VTQ_E_INTERNAL, "gguf: tensor rank > 8 (sanity bound)");
-        }
-        Tensor t;
-        t.numel = 1;
-        for (uint32_t d = 0; d < nd; d++) t.numel *= r.uint(8);
-        t.type = (uint32_t)r.uint(4);
-        offsets.emplace_back(name, r.uint(8));
-        ts[name] = t;
-    }
-    if (!r.ok()) {
-        *out = m;
-        return fail(m, VTQ_E_INTERNAL, "gguf: truncated");
-    }
-    const Meta* al = meta(kv, "general.alignment");
-    const uint64_t align = (al && al->type == 4) ? al->num : 32;
-    if (align == 0) {
-        *out = m;
-        return fail(m, VTQ_E_INTERNAL, "gguf: general.alignment is zero");
-    }
-    const size_t base = (r.pos() + align - 1) / align * align;
-    for (auto& [name, off] : offsets) {
-        Tensor& t = ts[name];
-        if (!tensor_bytes(t.type, t.numel, &t.nbytes)) {
-            *out = m;
-            return fail(m, VTQ_E_INTERNAL, "gguf: tensor size not a whole number of blocks");
-        }
-        t.offset = base + off;
-        if (t.offset + t.nbytes > len) {
-            *out = m;
-            return fail(m, VTQ_E_INTERNAL, "gguf: tensor extends past end of file");
-        }
-    }
-    // Config::from_gguf
-    const Meta* a = meta(kv, "general.architecture");
-    if (!a || a->type != 8) {
-        *out = m;
-        return fail(m, VTQ_E_INTERNAL, "gguf: missing 'general.architecture' metadata");
-    }
-    const std::string arch = a->str;
-    bool ok = read_usize(kv, arch + ".embedding_length", &m->dim) &&
-              read_usize(kv, arch + ".feed_forward_length", &m->hidden) &&
-              read_usize(kv, arch + ".block_count", &m->layers) &&
-              read_usize(kv, arch + ".attention.head_count", &m->heads) &&
-              read_usize(kv, arch + ".context_length", &m->seq);
-    if (ok && !read_usize(kv, arch + ".attention.head_count_kv", &m->kv_heads)) m->kv_heads = m->heads;
-    const Meta* toks = meta(kv, "tokenizer.ggml.tokens");
-    if (ok) {
-        if (toks && toks->type == 9)
-            m->vocab = (int)toks->count;
-        else
-            ok = read_usize(kv, arch + ".vocab_size", &m->vocab);
-    }
-    if (!ok || m->heads <= 0 || m->kv_heads <= 0 || m->dim % m->heads || m->heads % m->kv_heads) {
-        *out = m;
-        return fail(m, VTQ_E_INTERNAL, "gguf: numeric metadata missing or wrong type");
-    }
-    m->theta = read_f32(kv, arch + ".rope.freq_base", 10000.0f);
-    m->eps = read_f32(kv, arch + ".attention.layer_norm_rms_epsilon", 1e-5f);
-    m->neox = arch == "qwen2";
-    m->shared = ts.find("output.weight") == ts.end();
-    auto lin = [&](const std::string& n, Lin* o) {
-        auto it = ts.find(n);
-        if (it == ts.end()) return false;
-        o->type = (int)it->second.type;
-        o->offset = it->second.offset;
-        o->nbytes = it->second.nbytes;
-        return true;
-    };
-    auto f32 = [&](const std::string& n, size_t want, bool required, size_t* o) {
-        auto it = ts.find(n);
-        if (it == ts.end()) return !required;
-        if (it->second.type != 0 || it->second.nbytes != want * 4 || it->second.offset % 4) return false;
-        *o = it->second.offset;
-        return true;
-    };
+    auto* m = new (std::nothrow) vtqrt_model();
+    if (!m) return VTQ_E_GPU;
+    *out = m;
+    // GgufFile::parse, Config::from_gguf and QuantizedWeights::from_gguf on
+    // the host: a file that fails any check never reaches the device
+    static const uint8_t kEmpty[1] = {0};
+    vtq::gguf::File f;
+    vtq::gguf::Model md;
+    const char* msg = "";
+    int rc = vtq::gguf::parse(gguf ? gguf : kEmpty, len, &f, &msg);
+    if (!rc) rc = vtq::gguf::describe(f, &md, &msg);
+    if (rc) return fail(m, rc, msg);
+    m->dim = md.dim;
+    m->hidden = md.hidden;
+    m->layers = md.layers;
+    m->heads = md.heads;
+    m->kv_heads = md.kv_heads;
+    m->vocab = md.vocab;
+    m->seq = md.seq;
+    m->shared = md.shared;
+    m->neox = md.neox;
+    m->theta = md.theta;
+    m->eps = md.eps;
     const int head = m->dim / m->heads, kv_dim = m->kv_heads * head;
-    ok = lin("token_embd.weight", &m->tok) && f32("output_norm.weight", m->dim, true, &m->rms_final);
-    if (ok && !m->shared) ok = lin("output.weight", &m->wcls);
-    m->L.resize(m->layers);
-    for (int l = 0; ok && l < m->layers; l++) {
-        const std::string p = "blk." + std::to_string(l) + ".";
-        Layer& Ly = m->L[l];
-        ok = lin(p + "attn_q.weight", &Ly.wq) && lin(p + "attn_k.weight", &Ly.wk) && lin(p + "attn_v.weight", &Ly.wv) &&
-             lin(p + "attn_output.weight", &Ly.wo) && lin(p + "ffn_gate.weight", &Ly.w1) &&
-             lin(p + "ffn_down.weight", &Ly.w2) && lin(p + "ffn_up.weight", &Ly.w3) &&
-             f32(p + "attn_norm.weight", m->dim, true, &Ly.rms_att) &&
-             f32(p + "ffn_norm.weight", m->dim, true, &Ly.rms_ffn) && f32(p + "attn_q.bias", m->dim, false, &Ly.bq) &&
-             f32(p + "attn_k.bias", kv_dim, false, &Ly.bk) && f32(p + "attn_v.bias", kv_dim, false, &Ly.bv);
+
+    // device arena: every tensor the step reads, each copy 256-byte aligned;
+    // a bias is stored at the length it is added to, past its own end padded
+    // with -0.0 (add_bias zips the two slices, and v + -0.0 == v bit for bit)
+    size_t arena = 0;
+    auto place = [&](const vtq::gguf::View& v, size_t dev_bytes, Lin* o) {
+        if (v.type < 0) return;
+        o->type = v.type;
+        o->host = (size_t)v.offset;
+        o->nbytes = (size_t)v.nbytes;
+        o->dev = arena;
+        arena += (std::max<size_t>(dev_bytes, 1) + 255) / 256 * 256;
+    };
+    auto place_t = [&](const vtq::gguf::View& v, Lin* o) { place(v, (size_t)v.nbytes, o); };
+    place_t(md.tok, &m->tok);
+    place_t(md.rms_final, &m->rms_final);
+    if (!m->shared) place_t(md.wcls, &m->wcls);
+    m->L.resize((size_t)m->layers);
+    for (int l = 0; l < m->layers; l++) {
+        const vtq::gguf::LayerViews& V = md.L[(size_t)l];
+        Layer& Ly = m->L[(size_t)l];
+        place_t(V.rms_att, &Ly.rms_att);
+        place_t(V.rms_ffn, &Ly.rms_ffn);
+        place_t(V.wq, &Ly.wq);
+        place_t(V.wk, &Ly.wk);
+        place_t(V.wv, &Ly.wv);
+        place_t(V.wo, &Ly.wo);
+        place_t(V.w1, &Ly.w1);
+        place_t(V.w2, &Ly.w2);
+        place_t(V.w3, &Ly.w3);
+        place(V.bq, (size_t)m->dim * 4, &Ly.bq);
+        place(V.bk, (size_t)kv_dim * 4, &Ly.bk);
+        place(V.bv, (size_t)kv_dim * 4, &Ly.bv);
     }
-    if (!ok) {
-        *out = m;
-        return fail(m, VTQ_E_INTERNAL, "gguf: required Llama tensor not found");
-    }
-    int rc = vtq_create(device, &m->ctx);
-    if (rc) {
-        *out = m;
-        return fail(m, rc, m->ctx ? vtq_last_error(m->ctx) : "vtq_create failed");
-    }
+    arena += 256;  // the kernels fetch whole 16-byte chunks past a tensor's end
+
+    m->blob.assign(gguf, gguf + len);
+    if ((rc = vtq_create(device, &m->ctx))) return fail(m, rc, "vtq_create failed");
     if ((rc = hip_check(m, hipSetDevice(device), "hipSetDevice")) ||
         (rc = hip_check(m, hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking), "hipStreamCreate")) ||
-        (rc = hip_check(m, hipMalloc(&m->dblob, (len + 15) / 16 * 16 + 16), "hipMalloc(blob)")) ||
-        (rc = hip_check(m, hipMemcpy(m->dblob, m->blob.data(), len, hipMemcpyHostToDevice), "hipMemcpy(blob)"))) {
-        *out = m;
+        (rc = hip_check(m, hipMalloc(&m->dblob, arena), "hipMalloc(weights)")))
         return rc;
-    }
     m->device = device;
-    if ((rc = hip_check(m, hipDeviceGetAttribute(&m->num_cus, hipDeviceAttributeMultiprocessorCount, device),
-                        "hipDeviceGetAttribute"))) {
-        *out = m;
-        return rc;
+    std::vector<float> pad;
+    auto upload = [&](const Lin& t, size_t dev_floats) {
+        if (t.type < 0) return VTQ_OK;
+        if (!dev_floats)
+            return hip_check(m, hipMemcpy(m->dblob + t.dev, m->blob.data() + t.host, t.nbytes, hipMemcpyHostToDevice),
+                             "hipMemcpy(weights)");
+        pad.assign(dev_floats, -0.0f);
+        std::memcpy(pad.data(), m->blob.data() + t.host, std::min(t.nbytes, dev_floats * 4));
+        return hip_check(m, hipMemcpy(m->dblob + t.dev, pad.data(), dev_floats * 4, hipMemcpyHostToDevice),
+                         "hipMemcpy(bias)");
+    };
+    if ((rc = upload(m->tok, 0)) || (rc = upload(m->rms_final, 0)) || (rc = upload(m->wcls, 0))) return rc;
+    for (const Layer& Ly : m->L) {
+        for (const Lin* t : {&Ly.rms_att, &Ly.rms_ffn, &Ly.wq, &Ly.wk, &Ly.wv, &Ly.wo, &Ly.w1, &Ly.w2, &Ly.w3})
+            if ((rc = upload(*t, 0))) return rc;
+        if ((rc = upload(Ly.bq, (size_t)m->dim)) || (rc = upload(Ly.bk, (size_t)kv_dim)) ||
+            (rc = upload(Ly.bv, (size_t)kv_dim)))
+            return rc;
     }
-    const size_t kv_elems = (size_t)m->layers * m->seq * kv_dim;
+    if ((rc = hip_check(m, hipDeviceGetAttribute(&m->num_cus, hipDeviceAttributeMultiprocessorCount, device),
+                        "hipDeviceGetAttribute")))
+        return rc;
+    // RunState::new (forward.rs:28-34): k and v caches of layers * seq * kv_dim
+    size_t kv_elems = 0;
+    if (__builtin_mul_overflow((size_t)m->layers, (size_t)m->seq, &kv_elems) ||
+        __builtin_mul_overflow(kv_elems, (size_t)kv_dim, &kv_elems) || kv_elems > ((size_t)1 << 60))
+        return fail(m, VTQ_E_NOT_IMPLEMENTED, "vtq: KV cache size overflows");
     auto dalloc = [&](auto** p, size_t n) {
         return hip_check(m, hipMalloc(reinterpret_cast<void**>(p), std::max<size_t>(n, 1) * 4), "hipMalloc(state)");
     };
-    if ((rc = dalloc(&m->x, m->dim)) || (rc = dalloc(&m->xb, m->dim)) || (rc = dalloc(&m->qkv, m->dim + 2 * kv_dim)) ||
+    if ((rc = dalloc(&m->x, m->dim)) || (rc = dalloc(&m->xb, m->dim)) ||
+        (rc = dalloc(&m->qkv, (size_t)m->dim + 2 * (size_t)kv_dim)) ||
         (rc = dalloc(&m->att, m->dim)) || (rc = dalloc(&m->ffn, m->hidden)) || (rc = dalloc(&m->gate, m->hidden)) ||
         (rc = dalloc(&m->up, m->hidden)) || (rc = dalloc(&m->tmp, m->dim)) || (rc = dalloc(&m->logits, m->vocab)) ||
-        (rc = dalloc(&m->kc, kv_elems)) || (rc = dalloc(&m->vc, kv_elems)) || (rc = dalloc(&m->tokens, m->seq + 1)) ||
-        (rc = dalloc(&m->pos, 1)) || (rc = dalloc(&m->rope, head))) {
-        *out = m;
+        (rc = dalloc(&m->kc, kv_elems)) || (rc = dalloc(&m->vc, kv_elems)) ||
+        (rc = dalloc(&m->tokens, (size_t)m->seq + 1)) || (rc = dalloc(&m->pos, 1)) || (rc = dalloc(&m->rope, head)))
         return rc;
-    }
-    *out = m;
     return VTQ_OK;
 }
 
@@ -879,25 +761,88 @@ int vtqrt_load(int device, const uint8_t* gguf, size_t len, vtqrt_model** out) {
 
 namespace {
 
+// embedding_row's checks (forward_quantized.rs:818-919) for one token id
+int embed_check(vtqrt_model* m, uint32_t token) {
+    struct Fmt {
+        int type;
+        uint64_t elems, bytes;
+        const char *dim_msg, *row_msg;
+    };
+    static const Fmt kFmt[] = {
+        {2, 32, 18, "embedding_row Q4_0: dim must be a multiple of 32", "embedding_row Q4_0: row past end of table"},
+        {12, 256, 144, "embedding_row Q4_K: dim must be a multiple of 256", "embedding_row Q4_K: row past end of table"},
+        {14, 256, 210, "embedding_row Q6_K: dim must be a multiple of 256", "embedding_row Q6_K: row past end of table"},
+        {6, 32, 22, "embedding_row Q5_0: dim must be a multiple of 32", "embedding_row Q5_0: row past end of table"},
+        {8, 32, 34, "embedding_row Q8_0: dim must be a multiple of 32", "embedding_row Q8_0: row past end of table"},
+    };
+    // (row + 1) * row_bytes: below 2^33 * 2^33, so 128-bit arithmetic cannot wrap
+    const unsigned __int128 row = token, dim = (uint64_t)m->dim, len = m->tok.nbytes;
+    if (m->tok.type == 0)
+        return (row + 1) * dim * 4 > len ? fail(m, VTQ_E_INTERNAL, "embedding_row F32: table too small for token id")
+                                         : VTQ_OK;
+    for (const Fmt& f : kFmt) {
+        if (f.type != m->tok.type) continue;
+        if (dim % f.elems) return fail(m, VTQ_E_INTERNAL, f.dim_msg);
+        const unsigned __int128 row_bytes = dim / f.elems * f.bytes;
+        return (row + 1) * row_bytes > len ? fail(m, VTQ_E_INTERNAL, f.row_msg) : VTQ_OK;
+    }
+    return fail(m, VTQ_E_NOT_IMPLEMENTED, "embedding_row: non-Q4_0 / Q4_K / Q6_K / Q8_0 / F32 embedding dtype");
+}
+
+// The checks one step makes before its arithmetic, in the step's order:
+// rms_norm_slice's weight length (rms_norm.rs:80-85) and every
+// linear_dispatch arm's shape checks (vtq_linear_device validates and, with
+// batch 0, launches nothing).  Passing them is what makes the fused GEMVs'
+// row counts safe to launch.
+int step_check(vtqrt_model* m, int regime) {
+    const int dim = m->dim, kv_dim = m->kv_heads * (m->dim / m->heads), hidden = m->hidden;
+    auto norm = [&](const Lin& w) {
+        return w.nbytes / 4 != (size_t)dim
+                   ? fail(m, VTQ_E_SHAPE_MISMATCH, "expected weight length == last dim of x, got weight mismatch")
+                   : VTQ_OK;
+    };
+    auto lin = [&](const Lin& w, int in_feat, int out_feat) {
+        const int rc = vtq_linear_device(m->ctx, w.type, regime, nullptr, m->dblob + w.dev, w.nbytes, nullptr, 0,
+                                         (size_t)in_feat, (size_t)out_feat, m->stream);
+        return rc ? fail(m, rc, vtq_last_error(m->ctx)) : VTQ_OK;
+    };
+    int rc = VTQ_OK;
+    for (const Layer& Ly : m->L) {
+        if ((rc = norm(Ly.rms_att)) || (rc = lin(Ly.wq, dim, dim)) || (rc = lin(Ly.wk, dim, kv_dim)) ||
+            (rc = lin(Ly.wv, dim, kv_dim)) || (rc = lin(Ly.wo, dim, dim)) || (rc = norm(Ly.rms_ffn)) ||
+            (rc = lin(Ly.w1, dim, hidden)) || (rc = lin(Ly.w3, dim, hidden)) || (rc = lin(Ly.w2, hidden, dim)))
+            return rc;
+    }
+    if ((rc = norm(m->rms_final))) return rc;
+    return lin(m->shared ? m->tok : m->wcls, dim, m->vocab);
+}
+
 // run_quantized (inference.rs:274-345), optionally with the step recorders
 int run_impl(vtqrt_model* m, int regime, const char* model_id, const uint8_t weights_hash[32], const uint32_t* prompt,
-             int prompt_len, int n_new, float* logits, uint32_t* tokens, uint8_t digest[32], Recorder* rec) {
+             int prompt_len, int n_new, float* logits, uint32_t* tokens, uint8_t digest[32], uint8_t* digest_v1,
+             Recorder* rec) {
     if (!m || !m->ctx || !model_id || !weights_hash || !digest || (prompt_len > 0 && !prompt) ||
         (n_new > 0 && !tokens) || n_new < 0)
         return VTQ_E_INVALID_ARGUMENT;
     m->err.clear();
-    if (prompt_len <= 0) return fail(m, VTQ_E_INTERNAL, "prompt_tokens must not be empty");
-    const int total = prompt_len + n_new;
-    if (total > m->seq) return fail(m, VTQ_E_INTERNAL, "prompt + n_new_tokens exceeds seq_len");
-    if (!vtq::decode::embed_row_bytes(m->tok.type, m->dim))
-        return fail(m, VTQ_E_NOT_IMPLEMENTED, "embedding_row: non-Q4_0 / Q4_K / Q6_K / Q8_0 / F32 embedding dtype");
-    if ((m->dim / m->heads) % 2)
-        return fail(m, VTQ_E_NOT_IMPLEMENTED, "RoPE: odd head dimension");
-    const uint32_t rows = table_rows(m);
-    for (int i = 0; i < prompt_len; i++)
-        if (prompt[i] >= rows) return fail(m, VTQ_E_INTERNAL, "embedding_row: row past end of table");
-    int rc = hip_check(m, hipSetDevice(m->device), "hipSetDevice");
+    // run_quantized_with_sink's checks (inference.rs:301-311), in usize there
+    if (prompt_len <= 0) return fail(m, VTQ_E_INVALID_SHAPE, "prompt_tokens must not be empty");
+    const int64_t total64 = (int64_t)prompt_len + (int64_t)n_new;
+    if (total64 > (int64_t)m->seq) return fail(m, VTQ_E_INVALID_SHAPE, "prompt + n_new_tokens exceeds seq_len");
+    const int total = (int)total64;
+    // step 0 reports what any step would (embedding_row, then the step's
+    // norms and linears in order); later prompt tokens fail at their own step
+    int rc = embed_check(m, prompt[0]);
+    if (!rc) rc = step_check(m, regime);
+    for (int i = 1; !rc && i < prompt_len; i++) rc = embed_check(m, prompt[i]);
     if (rc) return rc;
+    const int head = m->dim / m->heads;
+    if (head % 2) return fail(m, VTQ_E_NOT_IMPLEMENTED, "vtq: odd head dimension (RoPE pairs)");
+    if (!vtq::decode::attention_supported(head, m->seq))
+        return fail(m, VTQ_E_NOT_IMPLEMENTED, "vtq: head dimension or context length beyond the attention kernel");
+    if (m->dim > 32768) return fail(m, VTQ_E_NOT_IMPLEMENTED, "vtq: model dimension above 32768 (rms_norm)");
+    const uint32_t rows = table_rows(m);
+    if ((rc = hip_check(m, hipSetDevice(m->device), "hipSetDevice"))) return rc;
     if (logits && m->hist_cap < (size_t)total * m->vocab) {
         if (m->hist) (void)hipFree(m->hist);
         m->hist = nullptr;
@@ -950,7 +895,7 @@ int run_impl(vtqrt_model* m, int regime, const char* model_id, const uint8_t wei
         }
         if (graph) (void)hipGraphDestroy(graph);
     }
-    rc = hip_check(m, vtq::decode::embed(m->tok.type, m->dblob + m->tok.offset, table_rows(m), m->tokens, m->pos, m->dim,
+    rc = hip_check(m, vtq::decode::embed(m->tok.type, m->dblob + m->tok.dev, table_rows(m), m->tokens, m->pos, m->dim,
                                          m->x, rope_args(m), m->stream),
                    "embedding_row");
     for (int pos = 0; pos < total && !rc; pos++) {
@@ -985,7 +930,7 @@ int run_impl(vtqrt_model* m, int regime, const char* model_id, const uint8_t wei
     if ((rc = hip_check(m, hipStreamSynchronize(m->stream), "hipStreamSynchronize"))) return rc;
     // a picked token that a step consumed must name a table row
     for (int i = 0; i < n_new; i++)
-        if (fed[i] >= rows) return fail(m, VTQ_E_INTERNAL, "embedding_row: row past end of table");
+        if (fed[i] >= rows) return embed_check(m, fed[i]);
     std::vector<uint32_t> gen(fed.begin() + 1, fed.end());
     std::memcpy(tokens, gen.data(), gen.size() * 4);
     // the receipt: inputs then outputs, length-prefixed (inference.rs:300-333)
@@ -999,53 +944,65 @@ int run_impl(vtqrt_model* m, int regime, const char* model_id, const uint8_t wei
     std::memcpy(ob.data(), gen.data(), ob.size());
     vtqrt_blake3(ob.data(), ob.size(), out_hash);
     const uint32_t n_new_u32 = (uint32_t)n_new;
+    // write_sections (builder.rs:491-519): the part v1 and v2 share
+    auto sections = [&](Blake3& h) {
+        auto field = [&](const char* name, const void* data, size_t n) {
+            leb128(h, std::strlen(name));
+            h.update(name, std::strlen(name));
+            leb128(h, n);
+            h.update(data, n);
+        };
+        leb128(h, 5);
+        field("model_id", model_id, std::strlen(model_id));
+        field("weights_hash", weights_hash, 32);
+        field("arch_hash", arch_hash, 32);
+        field("prompt_tokens", pb.data(), pb.size());
+        field("n_new_tokens", &n_new_u32, 4);
+        leb128(h, 2);
+        field("output_tokens", ob.data(), ob.size());
+        field("output_tokens_hash", out_hash, 32);
+        // ops and activations (write_op / write_activation, builder.rs:525-560); no interventions
+        const size_t n_ops = rec ? rec->ops.size() : 0, n_acts = rec ? rec->acts.size() : 0;
+        leb128(h, n_ops);
+        for (size_t i = 0; i < n_ops; i++) {
+            const vtqrt_op_record& o = rec->ops[i];
+            const size_t nl = std::strlen(o.op_name);
+            leb128(h, o.op_index);
+            leb128(h, nl);
+            h.update(o.op_name, nl);
+            leb128(h, o.layer);
+            h.update(o.input_hash, 32);
+            h.update(o.params_hash, 32);
+            h.update(o.output_hash, 32);
+        }
+        leb128(h, n_acts);
+        for (size_t i = 0; i < n_acts; i++) {
+            const vtqrt_act_record& a = rec->acts[i];
+            const size_t nl = std::strlen(a.checkpoint);
+            leb128(h, a.act_index);
+            leb128(h, a.token_index);
+            leb128(h, a.layer);
+            leb128(h, nl);
+            h.update(a.checkpoint, nl);
+            h.update(a.tensor_hash, 32);
+        }
+        leb128(h, 0);
+    };
+    // compute_digest (v2, builder.rs:458-471): the domain, then REGIME length-prefixed
     static const char kRegime[] = "vitni-regime-1";
     Blake3 h;
     h.update("vitnify-receipt v2\x00", 19);
     leb128(h, sizeof kRegime - 1);
     h.update(kRegime, sizeof kRegime - 1);
-    auto field = [&](const char* name, const void* data, size_t n) {
-        leb128(h, std::strlen(name));
-        h.update(name, std::strlen(name));
-        leb128(h, n);
-        h.update(data, n);
-    };
-    leb128(h, 5);
-    field("model_id", model_id, std::strlen(model_id));
-    field("weights_hash", weights_hash, 32);
-    field("arch_hash", arch_hash, 32);
-    field("prompt_tokens", pb.data(), pb.size());
-    field("n_new_tokens", &n_new_u32, 4);
-    leb128(h, 2);
-    field("output_tokens", ob.data(), ob.size());
-    field("output_tokens_hash", out_hash, 32);
-    // ops and activations (write_op / write_activation, builder.rs:525-560); no interventions
-    const size_t n_ops = rec ? rec->ops.size() : 0, n_acts = rec ? rec->acts.size() : 0;
-    leb128(h, n_ops);
-    for (size_t i = 0; i < n_ops; i++) {
-        const vtqrt_op_record& o = rec->ops[i];
-        const size_t nl = std::strlen(o.op_name);
-        leb128(h, o.op_index);
-        leb128(h, nl);
-        h.update(o.op_name, nl);
-        leb128(h, o.layer);
-        h.update(o.input_hash, 32);
-        h.update(o.params_hash, 32);
-        h.update(o.output_hash, 32);
-    }
-    leb128(h, n_acts);
-    for (size_t i = 0; i < n_acts; i++) {
-        const vtqrt_act_record& a = rec->acts[i];
-        const size_t nl = std::strlen(a.checkpoint);
-        leb128(h, a.act_index);
-        leb128(h, a.token_index);
-        leb128(h, a.layer);
-        leb128(h, nl);
-        h.update(a.checkpoint, nl);
-        h.update(a.tensor_hash, 32);
-    }
-    leb128(h, 0);
+    sections(h);
     h.final(digest);
+    // compute_digest_v1 (builder.rs:476-487): the frozen domain, no regime
+    if (digest_v1) {
+        Blake3 h1;
+        h1.update("vitnify-receipt v1\x00", 19);
+        sections(h1);
+        h1.final(digest_v1);
+    }
     return VTQ_OK;
 }
 
@@ -1055,8 +1012,9 @@ extern "C" {
 
 int vtqrt_run(vtqrt_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
               const uint32_t* prompt, int prompt_len, int n_new, float* logits, uint32_t* tokens,
-              uint8_t digest[32]) {
-    return run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, logits, tokens, digest, nullptr);
+              uint8_t digest[32], uint8_t digest_v1[32]) {
+    return run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, logits, tokens, digest, digest_v1,
+                    nullptr);
 }
 
 int vtqrt_run_recorded(vtqrt_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],
@@ -1067,7 +1025,7 @@ int vtqrt_run_recorded(vtqrt_model* m, int regime, const char* model_id, const u
     Recorder rec;
     rec.flags = flags;
     const int rc = run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, nullptr, tokens, digest,
-                            &rec);
+                            nullptr, &rec);
     if (rc) return rc;
     if (n_ops) *n_ops = rec.ops.size();
     if (n_acts) *n_acts = rec.acts.size();

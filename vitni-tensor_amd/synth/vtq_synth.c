@@ -213,7 +213,7 @@ typedef struct {
 
 static size_t gt_bytes(const gt_t *t) {
     const uint64_t rows = t->ne1 ? t->ne1 : 1;
-    switch (t->type) {
+    switch (t->type) {  /* 100: an F32 bias (written with type 0) */
     case 12: return (size_t)(rows * (t->ne0 / 256) * 144);
     case 14: return (size_t)(rows * (t->ne0 / 256) * 210);
     default: return (size_t)(rows * t->ne0 * 4);
@@ -222,7 +222,9 @@ static size_t gt_bytes(const gt_t *t) {
 
 size_t vtqs_llama_gguf(const vtqs_llama *c, uint64_t seed, uint8_t *out) {
     const uint32_t head = c->dim / c->heads, kv_dim = c->kv_heads * head;
-    const size_t nt = 3 + 9 * (size_t)c->layers;
+    const uint64_t align = c->alignment ? c->alignment : 32;
+    const char *arch = c->arch == 1 ? "qwen2" : "llama";
+    const size_t nt = 3 + 9 * (size_t)c->layers + (c->qkv_bias ? 3 * (size_t)c->layers : 0);
     gt_t *ts = (gt_t *)calloc(nt, sizeof(gt_t));
     size_t k = 0;
 #define T(NAME, TYPE, NE0, NE1)                                              \
@@ -238,64 +240,81 @@ size_t vtqs_llama_gguf(const vtqs_llama *c, uint64_t seed, uint8_t *out) {
         char nm[64];
         snprintf(nm, sizeof nm, "blk.%u.attn_norm.weight", l); T(nm, 0, c->dim, 0);
         snprintf(nm, sizeof nm, "blk.%u.attn_q.weight", l); T(nm, 12, c->dim, c->dim);
-        snprintf(nm, sizeof nm, "blk.%u.attn_k.weight", l); T(nm, 12, c->dim, kv_dim);
+        snprintf(nm, sizeof nm, "blk.%u.attn_k.weight", l); T(nm, 12, c->dim, kv_dim - (l == 0 ? c->short_rows : 0));
         snprintf(nm, sizeof nm, "blk.%u.attn_v.weight", l); T(nm, 12, c->dim, kv_dim);
         snprintf(nm, sizeof nm, "blk.%u.attn_output.weight", l); T(nm, 12, c->dim, c->dim);
         snprintf(nm, sizeof nm, "blk.%u.ffn_norm.weight", l); T(nm, 0, c->dim, 0);
         snprintf(nm, sizeof nm, "blk.%u.ffn_gate.weight", l); T(nm, 12, c->dim, c->hidden);
         snprintf(nm, sizeof nm, "blk.%u.ffn_up.weight", l); T(nm, 12, c->dim, c->hidden);
         snprintf(nm, sizeof nm, "blk.%u.ffn_down.weight", l); T(nm, 12, c->hidden, c->dim);
+        if (c->qkv_bias) {
+            /* the bias tensors: F32 with ne1 = 0, marked by type 100 until written */
+            snprintf(nm, sizeof nm, "blk.%u.attn_q.bias", l); T(nm, 100, c->dim, 0);
+            snprintf(nm, sizeof nm, "blk.%u.attn_k.bias", l); T(nm, 100, kv_dim, 0);
+            snprintf(nm, sizeof nm, "blk.%u.attn_v.bias", l); T(nm, 100, kv_dim, 0);
+        }
     }
     T("output_norm.weight", 0, c->dim, 0);
-    T("output.weight", 14, c->dim, c->vocab);
+    if (!c->tied) T("output.weight", 14, c->dim, c->vocab);
 #undef T
+    const size_t n_used = k;
     size_t off = 0;
-    for (size_t i = 0; i < nt; i++) {
+    for (size_t i = 0; i < n_used; i++) {
         ts[i].nbytes = gt_bytes(&ts[i]);
         ts[i].offset = off;
-        off += (ts[i].nbytes + 31) / 32 * 32;
+        off += (ts[i].nbytes + align - 1) / align * align;
     }
     gw_t g = {out, 0};
+    char key[96];
     gw_bytes(&g, "GGUF", 4);
     gw_u32(&g, 3);
-    gw_u64(&g, nt);
+    gw_u64(&g, n_used);
     gw_u64(&g, 11);
     gw_str(&g, "general.architecture");
     gw_u32(&g, 8);
-    gw_str(&g, "llama");
-    gw_kv_u32(&g, "general.alignment", 32);
-    gw_kv_u32(&g, "llama.embedding_length", c->dim);
-    gw_kv_u32(&g, "llama.feed_forward_length", c->hidden);
-    gw_kv_u32(&g, "llama.block_count", c->layers);
-    gw_kv_u32(&g, "llama.attention.head_count", c->heads);
-    gw_kv_u32(&g, "llama.attention.head_count_kv", c->kv_heads);
-    gw_kv_u32(&g, "llama.context_length", c->ctx);
-    gw_kv_u32(&g, "llama.vocab_size", c->vocab);
-    gw_kv_f32(&g, "llama.rope.freq_base", c->rope_theta);
-    gw_kv_f32(&g, "llama.attention.layer_norm_rms_epsilon", c->rms_eps);
-    for (size_t i = 0; i < nt; i++) {
+    gw_str(&g, arch);
+    gw_kv_u32(&g, "general.alignment", (uint32_t)align);
+#define KV_U32(SUFFIX, V) snprintf(key, sizeof key, "%s." SUFFIX, arch); gw_kv_u32(&g, key, V)
+#define KV_F32(SUFFIX, V) snprintf(key, sizeof key, "%s." SUFFIX, arch); gw_kv_f32(&g, key, V)
+    KV_U32("embedding_length", c->dim);
+    KV_U32("feed_forward_length", c->hidden);
+    KV_U32("block_count", c->layers);
+    KV_U32("attention.head_count", c->heads);
+    KV_U32("attention.head_count_kv", c->kv_heads);
+    KV_U32("context_length", c->ctx);
+    KV_U32("vocab_size", c->vocab);
+    KV_F32("rope.freq_base", c->rope_theta);
+    KV_F32("attention.layer_norm_rms_epsilon", c->rms_eps);
+#undef KV_U32
+#undef KV_F32
+    for (size_t i = 0; i < n_used; i++) {
         gw_str(&g, ts[i].name);
         gw_u32(&g, ts[i].ne1 ? 2 : 1);
         gw_u64(&g, ts[i].ne0);
         if (ts[i].ne1) gw_u64(&g, ts[i].ne1);
-        gw_u32(&g, ts[i].type);
+        gw_u32(&g, ts[i].type == 100 ? 0 : ts[i].type);
         gw_u64(&g, ts[i].offset);
     }
-    const size_t base = (g.pos + 31) / 32 * 32;
+    const size_t base = (g.pos + align - 1) / align * align;
     if (out) memset(out + g.pos, 0, base - g.pos);
     if (out) {
-        for (size_t i = 0; i < nt; i++) {
+        for (size_t i = 0; i < n_used; i++) {
             uint8_t *p = out + base + ts[i].offset;
             const uint64_t ts_seed = seed + i;
-            const size_t pad = (ts[i].nbytes + 31) / 32 * 32 - ts[i].nbytes;
+            const size_t pad = (ts[i].nbytes + align - 1) / align * align - ts[i].nbytes;
             if (ts[i].type == 12) {
                 vtqs_q4_k(ts_seed, p, ts[i].ne1, ts[i].ne0, 0.01f);
             } else if (ts[i].type == 14) {
                 vtqs_q6_k(ts_seed, p, ts[i].ne1, ts[i].ne0, 0.01f);
             } else {
-                float *f = (float *)p;
-                vtqs_normal_f32(ts_seed, f, ts[i].ne0, 0.05f);
-                for (uint64_t e = 0; e < ts[i].ne0; e++) f[e] = 1.0f + f[e];
+                /* F32 tensors may sit at any multiple of the alignment: write
+                 * them through a staging buffer */
+                float *v = (float *)malloc(ts[i].ne0 * sizeof(float));
+                vtqs_normal_f32(ts_seed, v, ts[i].ne0, ts[i].type == 100 ? 0.5f : 0.05f);
+                if (ts[i].type != 100)
+                    for (uint64_t e = 0; e < ts[i].ne0; e++) v[e] = 1.0f + v[e];
+                memcpy(p, v, ts[i].ne0 * sizeof(float));
+                free(v);
             }
             memset(p + ts[i].nbytes, 0, pad);
         }

@@ -49,11 +49,21 @@ void vtqs_tokens(uint64_t seed, uint32_t *out, size_t n, uint32_t vocab);
  *   output_norm.weight           F32  [dim]
  *   output.weight                Q6_K [dim, vocab]
  * (GGML order: the first dimension is the row length).  Blocks come from
- * the generators above with sigma 0.01; tensor i uses seed + i.  Returns
- * the blob size; writes it to out when out is not NULL. */
+ * the generators above with sigma 0.01; tensor i uses seed + i.  Options:
+ *   arch 1        general.architecture "qwen2" (qwen2.* keys; the loader
+ *                 then rotates NeoX split halves), 0 "llama"
+ *   tied 1        no output.weight: the head is token_embd (shared weights)
+ *   qkv_bias 1    blk.L.attn_q.bias [dim], attn_k.bias / attn_v.bias
+ *                 [kv_dim], F32 N(0, 0.5)
+ *   alignment     general.alignment (0: 32); tensor offsets are multiples
+ *                 of it, so a value below 16 places tensors off 16 bytes
+ *   short_rows    that many rows fewer in blk.0.attn_k.weight (a tensor
+ *                 shorter than its configured shape)
+ * Returns the blob size; writes it to out when out is not NULL. */
 typedef struct {
     uint32_t dim, hidden, layers, heads, kv_heads, vocab, ctx;
     float rope_theta, rms_eps;
+    uint32_t arch, tied, qkv_bias, alignment, short_rows;
 } vtqs_llama;
 size_t vtqs_llama_gguf(const vtqs_llama *cfg, uint64_t seed, uint8_t *out);
 

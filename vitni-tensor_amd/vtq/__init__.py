@@ -31,6 +31,7 @@ REGIME_INTEGER = 0       # std-parallel build: integer Q4_K
 REGIME_FLOAT_FUSED = 1   # default build: float-fused Q4_K
 
 OK, E_INTERNAL, E_GPU, E_NOT_IMPLEMENTED, E_INVALID_ARGUMENT = 0, 1, 2, 3, 4
+E_MALFORMED, E_TRUNCATED, E_OVERFLOW, E_SHAPE_MISMATCH, E_INVALID_SHAPE = 5, 6, 7, 8, 9
 
 
 class VtqError(Exception):
@@ -67,7 +68,43 @@ class InvalidArgument(VtqError):
     code = E_INVALID_ARGUMENT
 
 
-_ERRORS = {c.code: c for c in (Internal, GpuError, NotImplementedDtype, InvalidArgument)}
+class Malformed(VtqError):
+    """Error::Malformed -- a GGUF file that violates the format."""
+
+    code = E_MALFORMED
+
+
+class Truncated(VtqError):
+    """Error::Truncated -- a GGUF file that ends before a field."""
+
+    code = E_TRUNCATED
+
+
+class Overflow(VtqError):
+    """Error::Overflow -- a GGUF length or offset whose arithmetic overflows."""
+
+    code = E_OVERFLOW
+
+
+class ShapeMismatch(VtqError):
+    """Error::ShapeMismatch -- a norm weight whose length is not the model dimension."""
+
+    code = E_SHAPE_MISMATCH
+
+
+class InvalidShape(VtqError):
+    """Error::InvalidShape -- an empty prompt, or prompt + new tokens past seq_len."""
+
+    code = E_INVALID_SHAPE
+
+
+_ERRORS = {c.code: c for c in (Internal, GpuError, NotImplementedDtype, InvalidArgument, Malformed, Truncated,
+                               Overflow, ShapeMismatch, InvalidShape)}
+
+
+def error_class(code: int):
+    """The exception class of a libvtq / libvtq_runtime status code."""
+    return _ERRORS.get(code, GpuError)
 
 _lib: Optional[ctypes.CDLL] = None
 

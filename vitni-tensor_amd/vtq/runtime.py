@@ -7,10 +7,9 @@ import os
 
 import numpy as np
 
-from . import LIB_DIR, load_library, GpuError, Internal, InvalidArgument, NotImplementedDtype
+from . import LIB_DIR, load_library, error_class
 
 _rt = None
-_ERR = {1: Internal, 2: GpuError, 3: NotImplementedDtype, 4: InvalidArgument}
 
 
 def lib() -> ctypes.CDLL:
@@ -30,8 +29,10 @@ def lib() -> ctypes.CDLL:
         L.vtqrt_last_error.restype = ctypes.c_char_p
         L.vtqrt_dims.argtypes = [vp, vp]
         L.vtqrt_dims.restype = i
-        L.vtqrt_run.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, vp, vp, vp]
+        L.vtqrt_run.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, vp, vp, vp, vp]
         L.vtqrt_run.restype = i
+        L.vtqrt_parse.argtypes = [vp, sz, i, vp, ctypes.c_char_p, sz]
+        L.vtqrt_parse.restype = i
         L.vtqrt_run_recorded.argtypes = [vp, i, ctypes.c_char_p, vp, vp, i, i, i, vp, vp, sz, vp, sz,
                                          ctypes.POINTER(sz), ctypes.POINTER(sz), vp]
         L.vtqrt_run_recorded.restype = i
@@ -39,6 +40,8 @@ def lib() -> ctypes.CDLL:
         L.vtqrt_blake3.restype = None
         L.vtqrt_rms_norm_device.argtypes = [vp, vp, sz, ctypes.c_float, vp, vp]
         L.vtqrt_rms_norm_device.restype = i
+        L.vtqrt_transcendentals_device.argtypes = [vp, sz, vp, vp]
+        L.vtqrt_transcendentals_device.restype = i
         _rt = L
     return _rt
 
@@ -51,11 +54,32 @@ def blake3(data) -> bytes:
     return bytes(out)
 
 
+def parse(blob, level=0):
+    """vtqrt_parse on the host (no GPU needed): GgufFile::parse (level 0), or
+    with Config / QuantizedWeights (level 1).  (status, message, dims):
+    status 0 is Ok, else the include/vtq.h code of the reference's Error
+    variant; dims (level 1, status 0) is (dim, hidden, layers, heads,
+    kv_heads, vocab, seq_len)."""
+    b = np.ascontiguousarray(np.frombuffer(bytes(blob), dtype=np.uint8) if isinstance(blob, (bytes, bytearray))
+                             else blob, dtype=np.uint8)
+    dims = np.zeros(7, dtype=np.int32)
+    err = ctypes.create_string_buffer(256)
+    rc = lib().vtqrt_parse(b.ctypes.data if b.size else None, b.size, level, dims.ctypes.data, err, len(err))
+    return rc, err.value.decode(), tuple(int(d) for d in dims) if rc == 0 and level == 1 else None
+
+
 def rms_norm_device(x_ptr, w_ptr, n, eps, y_ptr, stream=None) -> None:
     """vtqrt_rms_norm_device: enqueue rms_norm_slice on device pointers."""
     rc = lib().vtqrt_rms_norm_device(x_ptr, w_ptr, n, float(eps), y_ptr, stream)
     if rc != 0:
         raise RuntimeError(f"vtqrt_rms_norm_device failed with status {rc}")
+
+
+def transcendentals_device(x_ptr, n, y_ptr, stream=None) -> None:
+    """vtqrt_transcendentals_device: y[7i + k] = f_k(x[i]) on the device."""
+    rc = lib().vtqrt_transcendentals_device(x_ptr, n, y_ptr, stream)
+    if rc != 0:
+        raise RuntimeError(f"vtqrt_transcendentals_device failed with status {rc}")
 
 
 RECORD_OPS = 1
@@ -86,6 +110,7 @@ class Model:
     """A GGUF model uploaded to one GPU (vtqrt_load)."""
 
     def __init__(self, blob, device: int = 0):
+        self.digest_v1 = None
         b = np.ascontiguousarray(blob, dtype=np.uint8)
         self.handle = ctypes.c_void_p()
         rc = lib().vtqrt_load(device, b.ctypes.data, b.size, ctypes.byref(self.handle))
@@ -93,22 +118,26 @@ class Model:
             msg = lib().vtqrt_last_error(self.handle).decode()
             lib().vtqrt_free(self.handle)
             self.handle = None
-            raise _ERR.get(rc, GpuError)(msg)
+            raise error_class(rc)(msg)
         dims = np.zeros(7, dtype=np.int32)
         lib().vtqrt_dims(self.handle, dims.ctypes.data)
         self.dim, self.hidden, self.layers, self.heads, self.kv_heads, self.vocab, self.seq_len = map(int, dims)
 
     def run(self, prompt, n_new, weights_hash: bytes, regime=0, model_id="vitni-receipt", want_logits=True):
-        """(generated tokens, v2 digest hex, logits [steps][vocab] or None)."""
+        """(generated tokens, v2 digest hex, logits [steps][vocab] or None);
+        digest_v1 then holds the frozen v1 digest of the same cert."""
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
         wh = np.frombuffer(bytes(weights_hash), dtype=np.uint8).copy()
         tokens = np.zeros(max(1, n_new), dtype=np.uint32)
         logits = np.zeros((prompt.size + n_new) * self.vocab, dtype=np.float32) if want_logits else None
         digest = (ctypes.c_uint8 * 32)()
+        digest_v1 = (ctypes.c_uint8 * 32)()
         rc = lib().vtqrt_run(self.handle, regime, model_id.encode(), wh.ctypes.data, prompt.ctypes.data, prompt.size,
-                             n_new, None if logits is None else logits.ctypes.data, tokens.ctypes.data, digest)
+                             n_new, None if logits is None else logits.ctypes.data, tokens.ctypes.data, digest,
+                             digest_v1)
         if rc:
-            raise _ERR.get(rc, GpuError)(lib().vtqrt_last_error(self.handle).decode())
+            raise error_class(rc)(lib().vtqrt_last_error(self.handle).decode())
+        self.digest_v1 = bytes(digest_v1).hex()
         if logits is not None:
             logits = logits.reshape(prompt.size + n_new, self.vocab)
         return tokens[:n_new], bytes(digest).hex(), logits
@@ -129,7 +158,7 @@ class Model:
                                       prompt.size, n_new, flags, tokens.ctypes.data, ops, len(ops), acts, len(acts),
                                       ctypes.byref(n_ops), ctypes.byref(n_acts), digest)
         if rc:
-            raise _ERR.get(rc, GpuError)(lib().vtqrt_last_error(self.handle).decode())
+            raise error_class(rc)(lib().vtqrt_last_error(self.handle).decode())
         return tokens[:n_new], bytes(digest).hex(), list(ops[:n_ops.value]), list(acts[:n_acts.value])
 
     def close(self):

@@ -26,7 +26,9 @@ class LlamaCfg(ctypes.Structure):
 
     _fields_ = [("dim", ctypes.c_uint32), ("hidden", ctypes.c_uint32), ("layers", ctypes.c_uint32),
                 ("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32), ("vocab", ctypes.c_uint32),
-                ("ctx", ctypes.c_uint32), ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+                ("ctx", ctypes.c_uint32), ("rope_theta", ctypes.c_float), ("rms_eps", ctypes.c_float),
+                ("arch", ctypes.c_uint32), ("tied", ctypes.c_uint32), ("qkv_bias", ctypes.c_uint32),
+                ("alignment", ctypes.c_uint32), ("short_rows", ctypes.c_uint32)]
 
 
 def lib() -> ctypes.CDLL:
@@ -137,9 +139,15 @@ E2E_PROMPT = 128
 E2E_NEW = 64
 
 
-def llama_gguf(cfg: dict, seed: int) -> np.ndarray:
-    """GGUF v3 blob of a random-init Llama model (synth/vtq_synth.h)."""
-    c = LlamaCfg(**cfg)
+def llama_gguf(cfg: dict, seed: int, arch: str = "llama", tied: bool = False, qkv_bias: bool = False,
+               alignment: int = 32, short_rows: int = 0) -> np.ndarray:
+    """GGUF v3 blob of a random-init Llama (or Qwen2-layout) model
+    (synth/vtq_synth.h): arch "qwen2" names the qwen2.* keys (NeoX RoPE),
+    tied drops output.weight (the head is token_embd), qkv_bias adds the
+    attention biases, alignment sets general.alignment, short_rows drops
+    rows from blk.0.attn_k.weight."""
+    c = LlamaCfg(**cfg, arch={"llama": 0, "qwen2": 1}[arch], tied=int(tied), qkv_bias=int(qkv_bias),
+                 alignment=alignment, short_rows=short_rows)
     n = lib().vtqs_llama_gguf(ctypes.byref(c), seed, None)
     out = np.empty(n, dtype=np.uint8)
     lib().vtqs_llama_gguf(ctypes.byref(c), seed, out.ctypes.data)
@@ -152,9 +160,10 @@ def tokens(seed: int, n: int, vocab: int) -> np.ndarray:
     return out
 
 
-def e2e_inputs(cfg: dict = None, prompt_len: int = E2E_PROMPT):
-    """(gguf blob, prompt ids) of the end-to-end configuration."""
+def e2e_inputs(cfg: dict = None, prompt_len: int = E2E_PROMPT, **variant):
+    """(gguf blob, prompt ids) of the end-to-end configuration; `variant`
+    passes llama_gguf's options (arch, tied, qkv_bias, alignment, short_rows)."""
     cfg = LLAMA_1B1 if cfg is None else cfg
-    blob = llama_gguf(cfg, SEED_BASE + E2E_INDEX)
+    blob = llama_gguf(cfg, SEED_BASE + E2E_INDEX, **variant)
     prompt = tokens(SEED_BASE + E2E_INDEX + X_SEED_OFFSET, prompt_len, cfg["vocab"])
     return blob, prompt
