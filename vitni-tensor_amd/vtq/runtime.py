@@ -111,7 +111,9 @@ class Model:
 
     def __init__(self, blob, device: int = 0):
         self.digest_v1 = None
-        b = np.ascontiguousarray(blob, dtype=np.uint8)
+        self.handle = None
+        b = np.ascontiguousarray(np.frombuffer(blob, dtype=np.uint8) if isinstance(blob, (bytes, bytearray))
+                                 else blob, dtype=np.uint8)
         self.handle = ctypes.c_void_p()
         rc = lib().vtqrt_load(device, b.ctypes.data, b.size, ctypes.byref(self.handle))
         if rc:
@@ -162,7 +164,7 @@ class Model:
         return tokens[:n_new], bytes(digest).hex(), list(ops[:n_ops.value]), list(acts[:n_acts.value])
 
     def close(self):
-        if self.handle:
+        if getattr(self, "handle", None):
             lib().vtqrt_free(self.handle)
             self.handle = None
 
