@@ -812,11 +812,21 @@ int vtqo_linear_dispatch(int ggml_type, int regime, const float *x, size_t x_len
                 y[b * out_feat + o] = vtqo_canonical_dot(x + b * in_feat, wf + o * in_feat, in_feat);
         return VTQO_OK;
     }
-    case 12: /* Q4_K, :698-726 */
+    case 12: /* Q4_K, :698-726: the std-parallel build calls the row-parallel
+              * function (and reports its errors) for out_feat >= PAR_MIN_ROWS
+              * whatever the thread count; the default build the fused one */
         if (regime == 1) return vtqo_linear_q4_k_fused(x, w, w_len, y, batch, in_feat, out_feat, 1, msg);
-        return vtqo_linear_q4_k_integer(x, w, w_len, y, batch, in_feat, out_feat, par, msg);
-    case 14: /* Q6_K, :727-750 */
-        return vtqo_linear_q6_k_integer(x, w, w_len, y, batch, in_feat, out_feat, par, msg);
+        if (out_feat >= 512)
+            return linear_kquant(ROW_Q4K_INT, Q4_K_BYTES, "linear_q4_k_integer_parallel: in_feat % 256",
+                                 "linear_q4_k_integer_parallel: weight shape", x, w, w_len, y, batch, in_feat,
+                                 out_feat, par, msg);
+        return vtqo_linear_q4_k_integer(x, w, w_len, y, batch, in_feat, out_feat, 1, msg);
+    case 14: /* Q6_K, :727-750: the same; the default build always the serial function */
+        if (regime == 0 && out_feat >= 512)
+            return linear_kquant(ROW_Q6K_INT, Q6_K_BYTES, "linear_q6_k_integer_parallel: in_feat % 256",
+                                 "linear_q6_k_integer_parallel: weight shape", x, w, w_len, y, batch, in_feat,
+                                 out_feat, par, msg);
+        return vtqo_linear_q6_k_integer(x, w, w_len, y, batch, in_feat, out_feat, regime == 0 ? par : 1, msg);
     case 8: /* Q8_0, :751-764 */
         return dispatch_rowwise(vtqo_dequantize_q8_0, Q8_0_BYTES, "Q8_0: in_feat must be a multiple of 32",
                                 "linear_dispatch Q8_0: weight blob too small", x, w, w_len, y, batch,

@@ -354,9 +354,18 @@ void vtq_destroy(vtq_ctx* c) {
 
 const char* vtq_last_error(const vtq_ctx* c) { return c ? c->err.c_str() : "vtq: null context"; }
 
+// The reference's dispatch names the row-parallel k-quant functions in its
+// errors only in the std-parallel build and for out_feat >= PAR_MIN_ROWS
+// (forward_quantized.rs:704-750); the default build always calls the serial
+// ones.
+static bool dispatch_serial_names(int regime, size_t out_feat) {
+    return regime == VTQ_REGIME_FLOAT_FUSED || out_feat < 512;
+}
+
 int vtq_linear(vtq_ctx* c, int type, int regime, const float* x, size_t x_len, const uint8_t* w, size_t w_len,
                float* y, size_t y_len, size_t batch, size_t in_feat, size_t out_feat) {
-    return linear_host(c, type, regime, x, x_len, w, w_len, y, y_len, batch, in_feat, out_feat, out_feat < 512);
+    return linear_host(c, type, regime, x, x_len, w, w_len, y, y_len, batch, in_feat, out_feat,
+                       dispatch_serial_names(regime, out_feat));
 }
 
 int vtq_linear_q4_k_integer(vtq_ctx* c, const float* x, size_t x_len, const uint8_t* w, size_t w_len, float* y,
@@ -405,7 +414,7 @@ int vtq_linear_device(vtq_ctx* c, int type, int regime, const float* d_x, const 
     if (!c) return VTQ_E_INVALID_ARGUMENT;
     c->err.clear();
     Plan p;
-    int rc = plan_linear(c, type, regime, w_len, batch, in_feat, out_feat, out_feat < 512, &p);
+    int rc = plan_linear(c, type, regime, w_len, batch, in_feat, out_feat, dispatch_serial_names(regime, out_feat), &p);
     if (rc) return rc;
     size_t nx = 0, ny = 0;
     if (!mul_ok(batch, in_feat, &nx) || !mul_ok(batch, out_feat, &ny))
