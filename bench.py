@@ -7,14 +7,22 @@ HBM.  Weights rotate over enough copies (> 512 MB) that every launch reads
 them from HBM, not from the 256 MB MALL.
 
 Prints ONE JSON line (rank 0).  `value` is whole-step throughput in GB/s of
-algorithmic bytes (packed weights + fp32 x in + fp32 y out).  `roofline`
-describes the dominant kernel: its average launch duration is K back-to-back
-launches bracketed by HIP events on the launch stream.  `cpu_baseline` is the pinned C restatement of
-the reference path (oracle/, the std-parallel row-parallel integer kernels)
-timed on this host's cores on the same inputs.
+algorithmic bytes (packed weights + fp32 x in + fp32 y out) over exactly
+--steps steps replayed from a HIP graph.  `roofline` describes the dominant
+kernel of the step (the slower of the pair, 4096x11008): its launch time is
+the median over >= 50 graph replays of back-to-back launches, bracketed by
+HIP events on the launch stream.  `cpu_baseline` is the pinned C
+restatement of the reference path (oracle/, the std-parallel row-parallel
+integer kernels) timed on this host's cores on the same inputs.
 
-Other configs (`--config NAME`) are for profiling; the main line is the
-default one.
+`configs` carries every BASELINE configuration measured in the same run:
+per kernel the median launch time over >= 50 graph replays with the weights
+rotated (HBM, the main figure) and with one copy (MALL-warm), the roofline
+fraction, whether the output is bit-identical to the oracle, and the oracle's
+CPU time on the same inputs.
+
+Other workloads (`--workload NAME`) time one configuration alone; they are
+what the rocprofv3 profiles run.
 """
 import argparse
 import json
@@ -46,6 +54,10 @@ KERNEL_NAME = {12: "kquant_rows_kernel<Q4K>", 14: "kquant_rows_kernel<Q6K>", 8: 
 INT8_MFMA_PEAK_TOPS = 5000.0
 
 
+CPU_THREAD_CAP = 16  # the GPU box's CPU share for one GPU (OMP_NUM_THREADS there is 16)
+LAUNCHES_PER_REPLAY = 100  # back-to-back launches per graph replay in the per-kernel medians
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -56,9 +68,15 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-rotate", action="store_true", help="reuse one weight copy (MALL-warm figure)")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a replayed HIP graph")
+    ap.add_argument("--reps", type=int, default=50, help="graph replays per median")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-config figures of the default line")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="only run 20 device-to-device copies of this many MiB (HBM counter calibration)")
     return ap.parse_args()
+
+
+def cpu_threads():
+    return min(len(os.sched_getaffinity(0)), CPU_THREAD_CAP)
 
 
 def calibrate_copy(mib):
@@ -76,151 +94,254 @@ def calibrate_copy(mib):
                       "copies": 20}), flush=True)
 
 
-def measured_ceilings(dw, step_bytes_per_launch, gemm_shape, steps):
-    """Reference points measured on this GPU in the same run (BASELINE.md asks
-    for a measured stream peak and MFMA peak beside the published ones):
-    * stream: a plain device-to-device copy (torch copy_) of each rotated
-      weight copy into one destination, read + write bytes counted: the HBM
-      rate of the simplest library kernel on buffers of this size, launch
-      floor included;
-    * mfma: hipBLASLt's int8 GEMM (torch._int_mm) at the prefill shape, the
-      int8 rate a vendor GEMM reaches (it computes a plain int32 product, not
-      the reference's Q4_K arithmetic)."""
+class Timer:
+    """Back-to-back launches captured in one HIP graph (unless eager) and
+    replayed; HIP events on the launch stream bracket each replay."""
+
+    def __init__(self, eager=False):
+        import torch
+
+        self.torch = torch
+        self.eager = eager
+        self.stream = torch.cuda.current_stream()
+
+    def per_launch_us(self, body, n, reps):
+        """[per-launch microseconds of each of `reps` replays of n launches]."""
+        torch = self.torch
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        out = []
+        if self.eager:
+            for _ in range(reps):
+                torch.cuda.synchronize()
+                e0.record(self.stream)
+                for k in range(n):
+                    body(k, self.stream.cuda_stream)
+                e1.record(self.stream)
+                torch.cuda.synchronize()
+                out.append(e0.elapsed_time(e1) / n * 1e3)
+            return out
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            cs = torch.cuda.current_stream().cuda_stream
+            for k in range(n):
+                body(k, cs)
+        g.replay()
+        torch.cuda.synchronize()
+        for _ in range(reps):
+            e0.record(self.stream)
+            g.replay()
+            e1.record(self.stream)
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1) / n * 1e3)
+        del g
+        return out
+
+
+def stream_ceiling(dw, timer, reps):
+    """A plain device-to-device copy (torch copy_) of the rotated weight
+    copies into one destination, read + write bytes counted: the HBM rate of
+    the simplest library kernel on buffers of this size, launch floor
+    included (BASELINE.md asks for a measured stream peak beside the
+    published one)."""
     import torch
 
-    out = {}
     flat = [w for copies in dw for w in copies]
     dst = torch.empty_like(flat[0])
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    n = max(steps, 20)
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for k in range(n):
-            dst[: flat[k % len(flat)].numel()].copy_(flat[k % len(flat)])
-    g.replay()
-    torch.cuda.synchronize()
-    e0.record()
-    g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) / n * 1e3
+    us = statistics.median(timer.per_launch_us(
+        lambda k, cs: dst[: flat[k % len(flat)].numel()].copy_(flat[k % len(flat)]), LAUNCHES_PER_REPLAY, reps))
     nbytes = 2 * statistics.mean(w.numel() for w in flat)
-    out["stream"] = {"kernel": "device-to-device copy of the rotated weight copies (graph-replayed), read + write",
-                     "bytes_per_launch": int(nbytes), "us_per_launch": round(us, 3),
-                     "gb_s": round(nbytes / us / 1e3, 1), "frac_of_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
-    if gemm_shape is not None and hasattr(torch, "_int_mm"):
-        m, k_, nn = gemm_shape
-        a = torch.randint(-127, 128, (m, k_), dtype=torch.int8, device=flat[0].device)
-        b = torch.randint(-127, 128, (k_, nn), dtype=torch.int8, device=flat[0].device)
-        try:
-            for _ in range(3):
-                torch._int_mm(a, b)
-            torch.cuda.synchronize()
-            e0.record()
-            for _ in range(20):
-                torch._int_mm(a, b)
-            e1.record()
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) / 20 * 1e3
-            tops = 2.0 * m * k_ * nn / us / 1e6
-            out["mfma"] = {"kernel": f"torch._int_mm int8 {m}x{k_} @ {k_}x{nn} -> int32 (hipBLASLt)",
-                           "us_per_launch": round(us, 3), "tops": round(tops, 1),
-                           "frac_of_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
-        except RuntimeError as e:  # not every build ships the int8 GEMM
-            out["mfma"] = {"unavailable": str(e)[:120]}
+    return {"kernel": "device-to-device copy of the rotated weight copies (graph-replayed), read + write",
+            "bytes_per_launch": int(nbytes), "us_per_launch": round(us, 3),
+            "gb_s": round(nbytes / us / 1e3, 1), "frac_of_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def mfma_ceiling(m, k_, nn, timer, reps):
+    """hipBLASLt's int8 GEMM (torch._int_mm) at the prefill shape: the int8
+    rate a vendor GEMM reaches (a plain int32 product, not the reference's
+    Q4_K arithmetic)."""
+    import torch
+
+    if not hasattr(torch, "_int_mm"):
+        return {"unavailable": "torch._int_mm missing"}
+    a = torch.randint(-127, 128, (m, k_), dtype=torch.int8, device="cuda:0")
+    b = torch.randint(-127, 128, (k_, nn), dtype=torch.int8, device="cuda:0")
+    try:
+        for _ in range(3):
+            torch._int_mm(a, b)
+        torch.cuda.synchronize()
+        us = statistics.median(Timer(eager=True).per_launch_us(lambda k, cs: torch._int_mm(a, b), 10, max(5, reps // 5)))
+    except RuntimeError as e:  # not every build ships the int8 GEMM
+        return {"unavailable": str(e)[:120]}
+    tops = 2.0 * m * k_ * nn / us / 1e6
+    return {"kernel": f"torch._int_mm int8 {m}x{k_} @ {k_}x{nn} -> int32 (hipBLASLt)",
+            "us_per_launch": round(us, 3), "tops": round(tops, 1), "frac_of_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4)}
+
+
+def cpu_time(fn, seconds, min_runs=3, max_runs=200):
+    """Median wall time of fn() after one warm-up, bounded to ~`seconds`."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+class Linear:
+    """One BASELINE linear configuration resident on the GPU: x, the weight
+    copies rotated over > 600 MB, y; launched through vtq_linear_device."""
+
+    def __init__(self, ctx, cfg, rotate=True):
+        import torch
+
+        self.ctx, self.c = ctx, cfg
+        self.x, self.w = cfg.make()
+        self.copies = 1 if not rotate else max(2, -(-ROTATE_MIN_BYTES // cfg.weight_bytes()))
+        dev = torch.device("cuda:0")
+        self.dx = torch.from_numpy(self.x).to(dev)
+        self.dw = [torch.from_numpy(self.w).to(dev) for _ in range(self.copies)]
+        self.dy = torch.empty(cfg.batch * cfg.out_feat, dtype=torch.float32, device=dev)
+
+    def launch(self, k, stream, copy=None):
+        c = self.c
+        w = self.dw[(k if copy is None else copy) % self.copies]
+        self.ctx.linear_device(c.ggml_type, 0, self.dx.data_ptr(), w.data_ptr(), w.numel(), self.dy.data_ptr(),
+                               c.batch, c.in_feat, c.out_feat, stream)
+
+    def bit_exact(self, threads):
+        import numpy as np
+        import torch
+
+        import oracle
+
+        c = self.c
+        self.dy.fill_(float("nan"))
+        self.launch(0, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        want = oracle.linear_dispatch(c.ggml_type, 0, self.x, self.w, c.batch, c.in_feat, c.out_feat, threads)
+        return bool(np.array_equal(self.dy.cpu().numpy().view(np.uint32), want.view(np.uint32)))
+
+    def release(self):
+        import torch
+
+        del self.dx, self.dw, self.dy
+        torch.cuda.empty_cache()
+
+
+def config_figures(ctx, cfg, timer, reps, cpu_seconds, with_cpu):
+    """Per-config figures: median launch time over `reps` graph replays of
+    100 back-to-back launches, weights rotated (HBM) and one copy (MALL-warm);
+    roofline fraction; bit-exactness vs the oracle; the oracle's CPU time."""
+    import oracle
+
+    L = Linear(ctx, cfg)
+    threads = cpu_threads()
+    exact = L.bit_exact(threads)
+    flushed = timer.per_launch_us(lambda k, s: L.launch(k, s), LAUNCHES_PER_REPLAY, reps)
+    warm = timer.per_launch_us(lambda k, s: L.launch(k, s, copy=0), LAUNCHES_PER_REPLAY, reps)
+    us, us_warm = statistics.median(flushed), statistics.median(warm)
+    gemm = cfg.batch >= 32
+    out = {"shape": f"{cfg.out_feat}x{cfg.in_feat} batch {cfg.batch}", "dtype": {12: "Q4_K", 14: "Q6_K",
+                                                                                  8: "Q8_0"}[cfg.ggml_type],
+           "us_per_launch_median": round(us, 3), "us_per_launch_min": round(min(flushed), 3),
+           "us_per_launch_mall_warm_median": round(us_warm, 3), "replays": reps,
+           "launches_per_replay": LAUNCHES_PER_REPLAY,
+           "weight_copies_rotated": L.copies, "bit_exact_vs_oracle": exact}
+    if gemm:
+        ops = 2.0 * cfg.batch * cfg.out_feat * cfg.in_feat
+        out.update({"bound": "mfma", "tops": round(ops / us / 1e6, 1), "peak_tops": INT8_MFMA_PEAK_TOPS,
+                    "frac": round(ops / us / 1e6 / INT8_MFMA_PEAK_TOPS, 4),
+                    "tops_mall_warm": round(ops / us_warm / 1e6, 1),
+                    "kernel": "q4k_gemm_kernel (+ act_quant_tiles_kernel)"})
+    else:
+        nb = cfg.algorithmic_bytes()
+        out.update({"bound": "hbm", "algorithmic_bytes": nb, "gb_s": round(nb / us / 1e3, 1),
+                    "peak_gb_s": HBM_PEAK_GBS, "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
+                    "gb_s_mall_warm": round(nb / us_warm / 1e3, 1),
+                    "kernel": KERNEL_NAME.get(cfg.ggml_type, "?")})
+    if with_cpu:
+        sec, n = cpu_time(lambda: oracle.linear_dispatch(cfg.ggml_type, 0, L.x, L.w, cfg.batch, cfg.in_feat,
+                                                         cfg.out_feat, threads), cpu_seconds)
+        if gemm:
+            out["cpu"] = {"tops": round(2.0 * cfg.batch * cfg.out_feat * cfg.in_feat / sec / 1e12, 4),
+                          "ms_per_call": round(sec * 1e3, 2), "cores": threads, "runs": n}
+        else:
+            out["cpu"] = {"gb_s": round(cfg.algorithmic_bytes() / sec / 1e9, 3), "ms_per_call": round(sec * 1e3, 3),
+                          "cores": threads, "runs": n}
+    L.release()
     return out
 
 
-def cpu_baseline(cfgs, inputs, seconds):
-    """The reference path restated in C (oracle), row-parallel on this host's cores."""
-    import oracle
-
-    threads = min(len(os.sched_getaffinity(0)), 16)
-    total_bytes = sum(c.algorithmic_bytes() for c in cfgs)
-
-    def step():
-        for c, (x, w) in zip(cfgs, inputs):
-            oracle.linear_dispatch(c.ggml_type, 0, x, w, c.batch, c.in_feat, c.out_feat, threads)
-
-    for _ in range(2):
-        step()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while len(times) < 10 or (time.perf_counter() < t_end and len(times) < 200):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    return {
-        "value": round(total_bytes / med / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": f"full workload, median of {len(times)} steps after 2 warm-ups "
-                  f"({med * 1e3:.1f} ms/step); oracle/vtq_oracle.c row-parallel integer kernels, "
-                  f"grain ceil(out/(4*threads)) as src/ops/quant.rs:1171",
-    }
+E2E_WEIGHT_BYTES = 22 * 24772608 + 53760000  # per step: every layer's Q4_K matrices + the Q6_K head
 
 
-def run_e2e(args):
-    """Config 5: inference::run_quantized of the 1.1B Llama (128 prompt ids +
-    64 new tokens) through libvtq_runtime, weights resident in HBM.  value =
-    decode steps per second over all 192 steps; the receipt digest and every
-    step's logits are checked against the CPU oracle."""
+def e2e_figures(reps, with_cpu):
+    """Config 5: inference::run_quantized of the 1.1B Llama (128 prompt ids
+    + 64 new tokens) through libvtq_runtime.  Tokens/s is decode steps per
+    second, median over `reps` runs (each run is what run_quantized returns:
+    tokens and receipt digest); one more run fetches every step's logits,
+    which with the digests are compared with the oracle's."""
     import numpy as np
 
     import oracle
     from vtq import runtime, synth
 
-    cfg = synth.LLAMA_1B1
     blob, prompt = synth.e2e_inputs()
     wh = runtime.blake3(blob)
     model = runtime.Model(blob)
     steps = synth.E2E_PROMPT + synth.E2E_NEW
-    model.run(prompt[:4], 4, wh, want_logits=False)  # warm-up: weights resident, kernels loaded
-    # timed: run_quantized's own outputs (tokens and receipt digest); the
-    # per-step logits are fetched in a separate, untimed run for the check
+    model.run(prompt[:4], 4, wh, want_logits=False)  # weights resident, kernels loaded
     times = []
-    for _ in range(max(1, min(args.steps, 3))):
+    for _ in range(reps):
         t0 = time.perf_counter()
         toks, digest, _ = model.run(prompt, synth.E2E_NEW, wh, want_logits=False)
         times.append(time.perf_counter() - t0)
+    digest_v1 = model.digest_v1
     toks_l, digest_l, logits = model.run(prompt, synth.E2E_NEW, wh)
     model.close()
-    sec = min(times)
-    threads = min(len(os.sched_getaffinity(0)), 16)
+    sec = statistics.median(times)
+    out = {"model": "llama-1.1B-shape", **synth.LLAMA_1B1, "prompt": synth.E2E_PROMPT, "new_tokens": synth.E2E_NEW,
+           "tokens_per_s_median": round(steps / sec, 2), "tokens_per_s_best": round(steps / min(times), 2),
+           "ms_per_token_median": round(sec / steps * 1e3, 4), "runs": reps, "receipt_digest": digest,
+           "receipt_digest_v1": digest_v1, "weight_bytes_per_step": E2E_WEIGHT_BYTES,
+           "gb_s": round(E2E_WEIGHT_BYTES * steps / sec / 1e9, 1),
+           "frac": round(E2E_WEIGHT_BYTES * steps / sec / 1e9 / HBM_PEAK_GBS, 4),
+           "ceiling_tokens_per_s": round(HBM_PEAK_GBS * 1e9 / E2E_WEIGHT_BYTES, 1)}
+    threads = cpu_threads()
     om = oracle.Model(blob)
     t0 = time.perf_counter()
     o_toks, o_digest, o_logits = om.run(prompt, synth.E2E_NEW, wh, threads=threads)
     cpu_sec = time.perf_counter() - t0
-    bit_exact = (digest == o_digest and digest_l == o_digest and bool(np.array_equal(toks, toks_l))
-                 and bool(np.array_equal(logits.view(np.uint32), o_logits.view(np.uint32))))
-    w_bytes = 22 * 24772608 + 53760000  # per step: every layer's Q4_K matrices + the Q6_K head
+    out["bit_exact_vs_oracle"] = bool(
+        digest == o_digest and digest_l == o_digest and digest_v1 == om.digest_v1 and np.array_equal(toks, toks_l)
+        and np.array_equal(toks, o_toks) and np.array_equal(logits.view(np.uint32), o_logits.view(np.uint32)))
+    if with_cpu:
+        out["cpu"] = {"tokens_per_s": round(steps / cpu_sec, 3), "cores": threads,
+                      "sample": f"the same 192-step run on oracle/vtq_oracle_e2e.c ({cpu_sec:.1f} s)"}
+    return out, steps, sec, toks
+
+
+def run_e2e(args):
+    """--workload e2e_decode: config 5 alone, as its own JSON line."""
+    from vtq import synth
+
+    fig, steps, sec, toks = e2e_figures(max(3, min(args.reps, 20)), not args.no_cpu)
     step_s = sec / steps
     out = {
         "metric": "E2E decode tokens/s (config 5), receipt digest bit-exact",
-        "value": round(steps / sec, 2),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": 1,
-        "ms_per_step": round(step_s * 1e3, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic random-init Llama GGUF (vtqs_llama_gguf, seeded) and prompt ids",
-        "config": {"workload": "e2e_decode", "model": "llama-1.1B-shape", **cfg, "prompt": synth.E2E_PROMPT,
-                   "new_tokens": synth.E2E_NEW, "receipt_digest": digest, "bit_exact_vs_oracle": bit_exact,
-                   "generated_tokens": [int(t) for t in toks[:8]]},
-        "roofline": {"bound": "hbm", "kernel": "whole decode step", "achieved": round(w_bytes / step_s / 1e9, 2),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(w_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_step": w_bytes,
-                     "ceiling_tokens_per_s": round(HBM_PEAK_GBS * 1e9 / w_bytes, 1)},
-        "cpu_baseline": {"value": round(steps / cpu_sec, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-                         "sample": f"the same 192-step run on oracle/vtq_oracle_e2e.c ({cpu_sec:.1f} s), linears "
-                                   f"row-parallel on {threads} threads"},
+        "value": round(steps / sec, 2), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": 1,
+        "ms_per_step": round(step_s * 1e3, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic random-init Llama GGUF (vtqs_llama_gguf, seeded) and prompt ids",
+        "config": {"workload": "e2e_decode", **fig, "generated_tokens": [int(t) for t in toks[:8]]},
+        "roofline": {"bound": "hbm", "kernel": "whole decode step", "achieved": round(E2E_WEIGHT_BYTES / step_s / 1e9, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(E2E_WEIGHT_BYTES / step_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_step": E2E_WEIGHT_BYTES},
     }
+    if "cpu" in fig:
+        out["cpu_baseline"] = {"value": fig["cpu"]["tokens_per_s"], "unit": "tokens/s", "cores": fig["cpu"]["cores"],
+                               "kind": "port", "sample": fig["cpu"]["sample"]}
     print(json.dumps(out), flush=True)
 
 
@@ -229,106 +350,60 @@ def main():
     if args.calibrate_copy_mib:
         calibrate_copy(args.calibrate_copy_mib)
         return
-    if args.workload == "e2e_decode" and args.gpus == 1:
-        run_e2e(args)
-        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the hot path shards by "
               f"output rows with no cross-device arithmetic, but multi-GPU runs are out of scope for this build.",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload == "e2e_decode":
+        run_e2e(args)
+        return
 
-    import numpy as np
     import torch
 
+    import oracle
     import vtq
     from vtq import synth
 
-    cfgs = [synth.CONFIGS[n] for n in WORKLOADS[args.workload]]
-    inputs = [c.make() for c in cfgs]
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
+    torch.cuda.set_device(torch.device("cuda:0"))
     ctx = vtq.Context(0)
-    stream = torch.cuda.current_stream()
-    sh = stream.cuda_stream
+    timer = Timer(eager=args.eager)
+    cfgs = [synth.CONFIGS[n] for n in WORKLOADS[args.workload]]
+    lins = [Linear(ctx, c, rotate=not args.no_rotate) for c in cfgs]
+    threads = cpu_threads()
+    bit_exact = all(L.bit_exact(threads) for L in lins)
 
-    step_weight_bytes = sum(c.weight_bytes() for c in cfgs)
-    copies = 1 if args.no_rotate else max(2, -(-ROTATE_MIN_BYTES // step_weight_bytes))
-    dx = [torch.from_numpy(x).to(dev) for x, _ in inputs]
-    dw = [[torch.from_numpy(w).to(dev) for _ in range(copies)] for _, w in inputs]
-    dy = [torch.empty(c.batch * c.out_feat, dtype=torch.float32, device=dev) for c in cfgs]
-
-    def launch(i, copy, sh):
-        c = cfgs[i]
-        ctx.linear_device(c.ggml_type, 0, dx[i].data_ptr(), dw[i][copy].data_ptr(), dw[i][copy].numel(),
-                          dy[i].data_ptr(), c.batch, c.in_feat, c.out_feat, sh)
-
-    def step(k, sh):
-        for i in range(len(cfgs)):
-            launch(i, k % copies, sh)
-
-    # parity of what is timed (outside the timed region)
-    import oracle
-
-    step(0, sh)
-    torch.cuda.synchronize()
-    bit_exact = True
-    for i, c in enumerate(cfgs):
-        x, w = inputs[i]
-        want = oracle.linear_dispatch(c.ggml_type, 0, x, w, c.batch, c.in_feat, c.out_feat,
-                                      min(len(os.sched_getaffinity(0)), 16))
-        bit_exact &= bool(np.array_equal(dy[i].cpu().numpy().view(np.uint32), want.view(np.uint32)))
+    def step(k, s):
+        for L in lins:
+            L.launch(k, s)
 
     for k in range(args.warmup):
-        step(k, sh)
+        step(k, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-
-    def timed_us(body):
-        """Average GPU time of one body(k, stream) over args.steps calls, the
-        calls issued back to back.  Unless --eager, the calls are captured in
-        a HIP graph and replayed, so host launch overhead cannot leave the GPU
-        idle between kernels of a few microseconds."""
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        if args.eager:
-            torch.cuda.synchronize()
-            e0.record(stream)
-            for k in range(args.steps):
-                body(k, sh)
-            e1.record(stream)
-        else:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                cs = torch.cuda.current_stream().cuda_stream
-                for k in range(args.steps):
-                    body(k, cs)
-            g.replay()
-            torch.cuda.synchronize()
-            e0.record(stream)
-            g.replay()
-            e1.record(stream)
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / args.steps * 1e3
-
-    # whole-step throughput: K steps back to back
-    ms_per_step = timed_us(step) * 1e-3
-    # per-kernel average launch duration: K back-to-back launches of each config alone
-    launch_us = [timed_us(lambda k, s, i=i: launch(i, k % copies, s)) for i in range(len(cfgs))]
-
+    # the main figure: exactly --steps steps, one replay
+    ms_per_step = timer.per_launch_us(step, args.steps, 1)[0] * 1e-3
+    # per-kernel launch times: median over --reps replays of 100 launches
+    launch_us = [statistics.median(timer.per_launch_us(lambda k, s, L=L: L.launch(k, s), LAUNCHES_PER_REPLAY,
+                                                       args.reps)) for L in lins]
     step_bytes = sum(c.algorithmic_bytes() for c in cfgs)
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    mean_launch_us = statistics.mean(launch_us)
-    per_launch_bytes = step_bytes / len(cfgs)
-    achieved = per_launch_bytes / (mean_launch_us * 1e-6) / 1e9
-    gemm = cfgs[0].batch >= 32
-    step_ops = sum(2 * c.batch * c.out_feat * c.in_feat for c in cfgs)
-
+    dom = max(range(len(cfgs)), key=lambda i: launch_us[i])  # the dominant (slowest) kernel of the step
+    dc = cfgs[dom]
+    gemm = dc.batch >= 32
+    if gemm:
+        ops = 2.0 * dc.batch * dc.out_feat * dc.in_feat
+        achieved, peak, unit = ops / launch_us[dom] / 1e6, INT8_MFMA_PEAK_TOPS, "TOPS"
+    else:
+        achieved, peak, unit = dc.algorithmic_bytes() / launch_us[dom] / 1e3, HBM_PEAK_GBS, "GB/s"
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    tkey = {"q4k_11008x4096": "q4k_gemv_11008x4096", "q4k_4096x11008": "q4k_gemv_4096x11008",
+            "q6k_32000x4096": "q6k_gemv_lm_head", "q8_0_4096x4096": "q8_0_gemv",
+            "q4k_gemm_14336x4096_m512": "q4k_gemm_prefill"}[dc.name]
     if os.path.exists(tpath):
-        t = json.load(open(tpath)).get(args.workload)
+        t = json.load(open(tpath)).get(tkey)
         if t:
             traffic = t.get("hbm_bytes_per_launch")
-
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -346,27 +421,57 @@ def main():
             "workload": args.workload,
             "shapes": [f"{c.out_feat}x{c.in_feat} batch {c.batch} {vtq.TYPE_NAMES[c.ggml_type]}" for c in cfgs],
             "bytes_per_step": step_bytes,
-            "weight_copies_rotated": copies,
-            "rotated_bytes": copies * step_weight_bytes,
+            "weight_copies_rotated": lins[0].copies,
+            "rotated_bytes": sum(L.copies * L.c.weight_bytes() for L in lins),
             "bit_exact_vs_oracle": bit_exact,
         },
         "roofline": {
             "bound": "mfma" if gemm else "hbm",
-            "kernel": "q4k_gemm_kernel (+ act_quant_tiles_kernel)" if gemm else KERNEL_NAME.get(cfgs[0].ggml_type, "?"),
-            "achieved": round(step_ops / len(cfgs) / (mean_launch_us * 1e-6) / 1e12, 2) if gemm else round(achieved, 2),
-            "peak": INT8_MFMA_PEAK_TOPS if gemm else HBM_PEAK_GBS,
-            "unit": "TOPS" if gemm else "GB/s",
-            "frac": round(step_ops / len(cfgs) / (mean_launch_us * 1e-6) / 1e12 / INT8_MFMA_PEAK_TOPS, 4) if gemm
-            else round(achieved / HBM_PEAK_GBS, 4),
+            "kernel": f"{'q4k_gemm_kernel' if gemm else KERNEL_NAME.get(dc.ggml_type, '?')} "
+                      f"{dc.out_feat}x{dc.in_feat} batch {dc.batch} (the step's slowest launch)",
+            "achieved": round(achieved, 2),
+            "peak": peak,
+            "unit": unit,
+            "frac": round(achieved / peak, 4),
             "traffic": traffic,
-            "launch_us_mean": [round(v, 3) for v in launch_us],
+            "launch_us_median": [round(v, 3) for v in launch_us],
             "bytes_per_launch": [c.algorithmic_bytes() for c in cfgs],
+            "replays_per_median": args.reps,
+            "launches_per_replay": LAUNCHES_PER_REPLAY,
+            "pair_frac": round(step_bytes / (sum(launch_us) * 1e-6) / 1e9 / HBM_PEAK_GBS, 4) if not gemm else None,
         },
     }
-    out["measured_ceilings"] = measured_ceilings(
-        dw, step_bytes / len(cfgs), (cfgs[0].batch, cfgs[0].in_feat, cfgs[0].out_feat) if gemm else None, args.steps)
+    ceilings = {"stream": stream_ceiling([L.dw for L in lins], timer, args.reps)}
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(cfgs, inputs, args.cpu_seconds)
+        def cpu_step():
+            for L in lins:
+                oracle.linear_dispatch(L.c.ggml_type, 0, L.x, L.w, L.c.batch, L.c.in_feat, L.c.out_feat, threads)
+
+        sec, n = cpu_time(cpu_step, args.cpu_seconds, min_runs=10)
+        out["cpu_baseline"] = {
+            "value": round(step_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"full workload, median of {n} steps after 1 warm-up ({sec * 1e3:.1f} ms/step); "
+                      f"oracle/vtq_oracle.c row-parallel integer kernels, grain ceil(out/(4*threads)) as "
+                      f"src/ops/quant.rs:1171; threads = online cores capped at {CPU_THREAD_CAP}, the GPU box's "
+                      f"CPU share per GPU"}
+    for L in lins:
+        L.release()
+    if args.workload == "q4k_gemv_ffn_pair" and not args.no_configs:
+        # every BASELINE configuration in the same run
+        figs = {}
+        for name in ("q8_0_4096x4096", "q4k_11008x4096", "q4k_4096x11008", "q6k_32000x4096",
+                     "q4k_gemm_14336x4096_m512"):
+            figs[name] = config_figures(ctx, synth.CONFIGS[name], timer, args.reps, 2.0, not args.no_cpu)
+            print(f"bench: {name} done", file=sys.stderr, flush=True)
+        fig5, _, _, _ = e2e_figures(20, not args.no_cpu)
+        figs["e2e_decode_llama_1b1"] = fig5
+        out["configs"] = figs
+        out["config"]["bit_exact_vs_oracle_all_configs"] = all(f["bit_exact_vs_oracle"] for f in figs.values())
+        g = synth.CONFIGS["q4k_gemm_14336x4096_m512"]
+        ceilings["mfma"] = mfma_ceiling(g.batch, g.in_feat, g.out_feat, timer, args.reps)
+    elif gemm:
+        ceilings["mfma"] = mfma_ceiling(dc.batch, dc.in_feat, dc.out_feat, timer, args.reps)
+    out["measured_ceilings"] = ceilings
     ctx.close()
     print(json.dumps(out), flush=True)
 
