@@ -133,6 +133,25 @@ int vtq_linear_device(vtq_ctx *ctx, int ggml_type, int regime, const float *d_x,
                       const uint8_t *d_w, size_t w_len, float *d_y, size_t batch, size_t in_feat,
                       size_t out_feat, void *stream);
 
+/* ---- allocation-free device entry point ----
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same computation, arguments and
+ * errors as vtq_linear_device, but it calls no hipMalloc / hipFree: the
+ * prefill GEMM's workspace (the quantized activations, batch >= 32 on Q4_K
+ * in the integer regime) lives in a fixed 32 MiB array on each GPU,
+ * allocated when the library loads.  Requests whose workspace would exceed
+ * it (vtq::q4k_gemm_workspace_bytes: about batch x in_feat x 1.08 bytes,
+ * batch capped at 8192 per chunk) return VTQ_E_NOT_IMPLEMENTED with a
+ * message and launch nothing.  All calls on one GPU share that array:
+ * calls that overlap in time on one device (any context, any stream) race
+ * on it and must be serialised by the caller.  Every byte a call reads from
+ * the array is written earlier in the same call, so nothing needs clearing
+ * between calls. */
+int vtq_linear_device_noalloc(vtq_ctx *ctx, int ggml_type, int regime, const float *d_x,
+                              const uint8_t *d_w, size_t w_len, float *d_y, size_t batch,
+                              size_t in_feat, size_t out_feat, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,11 +9,9 @@
 #include <climits>
 #include <cstdio>
 #include <cstring>
-#include <map>
 #include <mutex>
 #include <string>
 #include <unordered_map>
-#include <utility>
 
 #include "../../include/vtq.h"
 #include "vtq_kernels.h"
@@ -32,12 +30,20 @@ struct CachedWeight {
 
 }  // namespace
 
+// The GEMM workspace of vtq_linear_device_noalloc: one fixed array per GPU
+// (each device that loads the library holds its own copy until the process
+// ends).  Host code never passes `scratch` itself to a kernel: its address
+// on each device comes from hipGetSymbolAddress (vtq_create).
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 struct vtq_ctx {
     int device = 0;
     int num_cus = 0;
     hipStream_t stream = nullptr;
     DevBuf dx, dy;          // device staging for the host-pointer path
     DevBuf ws;              // kernel workspace (quantized activations of the GEMM path)
+    void* scratch_ptr = nullptr;  // this device's `scratch` (vtq_linear_device_noalloc)
     void* hx = nullptr;     // pinned staging
     size_t hx_cap = 0;
     void* hy = nullptr;
@@ -185,9 +191,11 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
     return VTQ_OK;
 }
 
-// Enqueue the kernels of a validated plan.
+// Enqueue the kernels of a validated plan.  `fixed_ws` (when not null) is a
+// caller-provided GEMM workspace already checked to be large enough; else the
+// context's workspace grows on demand.
 int run_plan(vtq_ctx* c, const Plan& p, const float* dx, const uint8_t* dw, float* dy, size_t batch,
-             size_t in_feat, size_t out_feat, hipStream_t s) {
+             size_t in_feat, size_t out_feat, hipStream_t s, void* fixed_ws = nullptr) {
     if (batch == 0 || out_feat == 0) return VTQ_OK;
     hipError_t e = hipSuccess;
     if (in_feat == 0) {  // every reduction is over nothing: fixed_tree([]) == 0.0
@@ -196,9 +204,13 @@ int run_plan(vtq_ctx* c, const Plan& p, const float* dx, const uint8_t* dw, floa
     }
     if (p.kind == Plan::kQ4KGemm) {
         // the launcher walks the batch in chunks that fit the workspace
-        int rc = grow_dev(c, c->ws, vtq::q4k_gemm_workspace_bytes((int)batch, (int)in_feat));
-        if (rc) return rc;
-        e = vtq::launch_q4k_gemm(dx, dw, dy, (int)batch, (int)in_feat, (int)out_feat, c->ws.ptr, s);
+        void* ws = fixed_ws;
+        if (!ws) {
+            int rc = grow_dev(c, c->ws, vtq::q4k_gemm_workspace_bytes((int)batch, (int)in_feat));
+            if (rc) return rc;
+            ws = c->ws.ptr;
+        }
+        e = vtq::launch_q4k_gemm(dx, dw, dy, (int)batch, (int)in_feat, (int)out_feat, ws, s);
         return e == hipSuccess ? VTQ_OK : hip_fail(c, e, "kernel launch");
     }
     const size_t kMaxGridY = 65535;
@@ -298,15 +310,26 @@ namespace vtq {
 
 hipError_t allow_dynamic_lds(const void* kernel, size_t bytes) {
     if (bytes <= 65536) return hipSuccess;
+    // (device, kernel) -> limit set; a fixed table (no heap: the no-alloc
+    // entry point runs through here), set anew every launch once it is full
+    struct Raised {
+        int dev;
+        const void* kernel;
+        size_t bytes;
+    };
     static std::mutex mu;
-    static std::map<std::pair<int, const void*>, size_t> raised;  // (device, kernel) -> limit set
+    static Raised raised[128];
+    static int n_raised = 0;
     int dev = 0;
     if (hipError_t e = hipGetDevice(&dev)) return e;
     std::lock_guard<std::mutex> lock(mu);
-    size_t& have = raised[{dev, kernel}];
-    if (have >= bytes) return hipSuccess;
+    Raised* slot = nullptr;
+    for (int i = 0; i < n_raised; i++)
+        if (raised[i].dev == dev && raised[i].kernel == kernel) slot = &raised[i];
+    if (slot && slot->bytes >= bytes) return hipSuccess;
     if (hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes)) return e;
-    have = bytes;
+    if (!slot && n_raised < 128) slot = &raised[n_raised++];
+    if (slot) *slot = Raised{dev, kernel, bytes};
     return hipSuccess;
 }
 
@@ -331,6 +354,12 @@ int vtq_create(int device, vtq_ctx** out) {
         c->num_cus <= 0)
         c->num_cus = 256;
     if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return VTQ_E_GPU;
+    }
+    // this device's copy of `scratch` (the device is current)
+    if (hipGetSymbolAddress(&c->scratch_ptr, HIP_SYMBOL(scratch)) != hipSuccess || !c->scratch_ptr) {
+        (void)hipStreamDestroy(c->stream);
         delete c;
         return VTQ_E_GPU;
     }
@@ -425,6 +454,27 @@ int vtq_linear_device(vtq_ctx* c, int type, int regime, const float* d_x, const 
     hipError_t e = hipSetDevice(c->device);
     if (e != hipSuccess) return hip_fail(c, e, "hipSetDevice");
     return run_plan(c, p, d_x, d_w, d_y, batch, in_feat, out_feat, static_cast<hipStream_t>(stream));
+}
+
+int vtq_linear_device_noalloc(vtq_ctx* c, int type, int regime, const float* d_x, const uint8_t* d_w, size_t w_len,
+                              float* d_y, size_t batch, size_t in_feat, size_t out_feat, void* stream) {
+    if (!c) return VTQ_E_INVALID_ARGUMENT;
+    c->err.clear();
+    Plan p;
+    int rc = plan_linear(c, type, regime, w_len, batch, in_feat, out_feat, dispatch_serial_names(regime, out_feat), &p);
+    if (rc) return rc;
+    size_t nx = 0, ny = 0;
+    if (!mul_ok(batch, in_feat, &nx) || !mul_ok(batch, out_feat, &ny))
+        return set_err(c, VTQ_E_INTERNAL, "vtq: batch * features overflows");
+    if ((nx && !d_x) || (ny && !d_y) || (p.w_need && !d_w)) return set_err(c, VTQ_E_INVALID_ARGUMENT, "vtq: null pointer");
+    if ((reinterpret_cast<uintptr_t>(d_x) & 15u) || (reinterpret_cast<uintptr_t>(d_w) & 15u))
+        return set_err(c, VTQ_E_INVALID_ARGUMENT, "vtq: device x and w must be 16-byte aligned");
+    if (p.kind == Plan::kQ4KGemm && vtq::q4k_gemm_workspace_bytes((int)batch, (int)in_feat) > kScratchBytes)
+        return set_err(c, VTQ_E_NOT_IMPLEMENTED,
+                       "vtq_linear_device_noalloc: the GEMM workspace of batch x in_feat exceeds the 32 MiB scratch");
+    hipError_t e = hipSetDevice(c->device);
+    if (e != hipSuccess) return hip_fail(c, e, "hipSetDevice");
+    return run_plan(c, p, d_x, d_w, d_y, batch, in_feat, out_feat, static_cast<hipStream_t>(stream), c->scratch_ptr);
 }
 
 }  // extern "C"

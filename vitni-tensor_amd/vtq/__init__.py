@@ -153,7 +153,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
 EXPORTED = (
     "vtq_create", "vtq_destroy", "vtq_last_error", "vtq_version", "vtq_linear",
     "vtq_linear_q4_k_integer", "vtq_linear_q6_k_integer", "vtq_linear_q4_k_fused",
-    "vtq_linear_q4_0", "vtq_release_weights", "vtq_linear_device",
+    "vtq_linear_q4_0", "vtq_release_weights", "vtq_linear_device", "vtq_linear_device_noalloc",
 )
 
 
