@@ -420,6 +420,202 @@ __global__ __launch_bounds__(64 * (PcWin<Dec, CPW>::NPW + 1)) void canon_pc_kern
     }
 }
 
+// ---- Q8_0 rows of at most 4096 inputs: the whole workgroup share in LDS ----
+//
+// The windowed kernel above keeps a window's raw bytes in registers four
+// windows ahead and stages them through LDS.  A workgroup's share of a Q8_0
+// layer of in_feat <= 4096 (8 rows of at most 128 blocks of 34 bytes, and x)
+// fits in LDS, so here every load is issued at the start, straight into LDS
+// (buffer loads with the lds bit), in window order, and no window waits on a
+// load issued late or on a staging pass.  The per-window round trip (products
+// written to LDS, barrier, read by the consumer) still bounds the loop.
+// Layout:
+//   per window w (256 elements, 8 blocks of each row), 3328 bytes
+//     [0, 2048)     codes: row r, block b at r*256 + b*32 (the 32 int8 codes,
+//                   moved to an aligned place by two 16-byte loads from the
+//                   2-byte-aligned block + 2)
+//     [2048, 3072)  x[256w .. 256w+255]
+//     [3072, 3328)  the 4 bytes at each block's start (d in the low half),
+//                   row r block b at 4(8r + b)
+// Producer wave p (1..4) issues the loads of part p-1 of every window in
+// window order, so before window w it waits for vmcnt(nwin - 1 - w) of its
+// own loads, and the barrier that follows makes the window visible to all.
+// Eight producer waves (waves 5..8 issue no loads) each form 4 products per
+// lane and window.
+// Products (x_i * w_i with w_i = d * q_i, exact in binary32) go to a
+// double-buffered chain-major buffer; the consumer wave adds them to its 64
+// chains (8 rows x 8 lanes) in the reference's order, as canon_pc_kernel.
+constexpr int kQ8WinBytes = 3328;
+constexpr int kQ8ChainStride = 36;  // floats between two chains of the product buffer
+constexpr int kQ8ProdBytes = 8 * 8 * kQ8ChainStride * 4;
+
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// One buffer load straight into LDS: lane L's SIZE bytes (16 or 4) from
+// buffer offset voff land at LDS byte lds_addr + SIZE * L.  Written as asm
+// so that the compiler does not track it: it would otherwise wait for every
+// such load (vmcnt(0)) before the first barrier or LDS read.  The kernel
+// orders these loads itself with explicit vmcnt waits and barriers; the
+// hardware completes loads in order, so the compiler's own waits on any
+// later load stay correct.
+template <int SIZE>
+__device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t lds_addr) {
+    static_assert(SIZE == 16 || SIZE == 4, "dwordx4 or dword");
+    if constexpr (SIZE == 16)
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                     :
+                     : "v"(voff), "s"(rs), "s"(lds_addr)
+                     : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
+                     :
+                     : "v"(voff), "s"(rs), "s"(lds_addr)
+                     : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
+// and lgkmcnt left at their maxima, so nothing else is waited for)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// the same for a count known only after unrolling (0 .. 15)
+__device__ __forceinline__ void wait_vmcnt_upto15(int n) {
+    switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<1>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    case 4: wait_vmcnt<4>(); break;
+    case 5: wait_vmcnt<5>(); break;
+    case 6: wait_vmcnt<6>(); break;
+    case 7: wait_vmcnt<7>(); break;
+    case 8: wait_vmcnt<8>(); break;
+    case 9: wait_vmcnt<9>(); break;
+    case 10: wait_vmcnt<10>(); break;
+    case 11: wait_vmcnt<11>(); break;
+    case 12: wait_vmcnt<12>(); break;
+    case 13: wait_vmcnt<13>(); break;
+    case 14: wait_vmcnt<14>(); break;
+    default: wait_vmcnt<15>(); break;
+    }
+}
+
+template <int NWIN>
+__global__ __launch_bounds__(576) void q8_lds_kernel(const float* __restrict__ x, const uint8_t* __restrict__ W,
+                                                      size_t row_bytes, float* __restrict__ y, int n, int out_feat) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    uint8_t* const win = lds;                                  // NWIN windows
+    float* const prod = reinterpret_cast<float*>(lds + NWIN * kQ8WinBytes);  // 2 buffers
+    const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const int row0 = blockIdx.x * 8;
+    const int nrows = min(8, out_feat - row0);
+    if (wave > 0 && wave <= 4) {
+        // the loads: part p of window w is one instruction of this wave
+        const int part = wave - 1;
+        const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(W + (size_t)row0 * row_bytes), (short)0, (int)(row_bytes * (size_t)nrows), 0x00020000);
+        const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(x + (size_t)blockIdx.y * n), (short)0, 4 * n, 0x00020000);
+        // per-lane source offsets at window 0; each window adds 272 bytes of every row (8 blocks) or 1 KB of x
+        uint32_t off;
+        if (part < 2) {
+            const int r = 4 * part + (lane >> 4), b = (lane & 15) >> 1, h = lane & 1;
+            off = (uint32_t)(r * row_bytes) + 34u * b + 2u + 16u * h;
+        } else if (part == 2) {
+            off = 16u * lane;
+        } else {
+            const int r = lane >> 3, b = lane & 7;
+            off = (uint32_t)(r * row_bytes) + 34u * b;
+        }
+        // LDS byte address of part p in window 0
+        const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)win + 1024u * part;
+#pragma unroll
+        for (int w = 0; w < NWIN; w++) {
+            const uint32_t dst = lds0 + (uint32_t)(w * kQ8WinBytes);
+            if (part < 2) load_to_lds<16>(rw, off + 272u * w, dst);
+            else if (part == 2) load_to_lds<16>(rx, off + 1024u * w, dst);
+            else load_to_lds<4>(rw, off + 272u * w, dst);
+        }
+    }
+    // window 0 in LDS
+    if (wave > 0 && wave <= 4) wait_vmcnt<NWIN - 1>();
+    __syncthreads();
+    if (wave == 0) {
+        // consumer: lane = row r (lane / 8), chain j (lane % 8)
+        const int r = lane >> 3, j = lane & 7;
+        float acc = 0.0f;
+        __syncthreads();  // step 0: the producers form window 0
+#pragma unroll
+        for (int s = 1; s <= NWIN; s++) {
+            const float* pp = prod + ((s - 1) & 1) * (8 * 8 * kQ8ChainStride) + (r * 8 + j) * kQ8ChainStride;
+            float4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = reinterpret_cast<const float4*>(pp)[i];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                acc = acc + v[i].x;
+                acc = acc + v[i].y;
+                acc = acc + v[i].z;
+                acc = acc + v[i].w;
+            }
+            __syncthreads();
+        }
+        const float t = group_tree<1, 8>(acc);  // fixed_tree over the 8 chains
+        if (j == 0 && r < nrows) y[(size_t)blockIdx.y * out_feat + row0 + r] = t;
+        return;
+    }
+    // producers: lane L -> row r, block b of the window, elements k .. k+3 of the block
+    // (chains k % 8 .. k % 8 + 3, position 4b + k / 8)
+    const int L = tid - 64, r = L >> 6, b = (L >> 3) & 7, k = 4 * (L & 7);
+    float* const pdst0 = prod + r * 8 * kQ8ChainStride + (4 * b + (k >> 3)) + (k & 7) * kQ8ChainStride;
+#pragma unroll
+    for (int s = 0; s <= NWIN; s++) {
+        if (s < NWIN) {
+            const uint8_t* wb = win + s * kQ8WinBytes;
+            const uint32_t cq = *reinterpret_cast<const uint32_t*>(wb + r * 256 + b * 32 + k);
+            const float d = f16_hw(*reinterpret_cast<const uint16_t*>(wb + 3072 + 4 * (8 * r + b)));
+            const float4 x0 = *reinterpret_cast<const float4*>(wb + 2048 + 4 * (32 * b + k));
+            const float xa[4] = {x0.x, x0.y, x0.z, x0.w};
+            float* pd = pdst0 + (s & 1) * (8 * 8 * kQ8ChainStride);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = (int)(int8_t)(uint8_t)(cq >> (8 * i));
+                const float wv = d * (float)q;  // exact: an f16 times an int8
+                pd[i * kQ8ChainStride] = xa[i] * wv;
+            }
+        }
+        if (s + 1 < NWIN && wave <= 4) wait_vmcnt_upto15(NWIN - 2 - s);
+        __syncthreads();
+    }
+}
+
+// 8 rows per workgroup: one consumer wave and eight producer waves
+static size_t q8_lds_bytes(int nwin) { return (size_t)nwin * kQ8WinBytes + 2 * kQ8ProdBytes; }
+
+template <int NWIN>
+static hipError_t launch_q8_lds_n(const float* x, const uint8_t* w, size_t row_bytes, float* y, int batch, int n,
+                                  int out_feat, hipStream_t stream) {
+    const size_t lds = q8_lds_bytes(NWIN);
+    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(q8_lds_kernel<NWIN>), lds)) return e;
+    dim3 grid((unsigned)((out_feat + 7) / 8), (unsigned)batch, 1);
+    hipLaunchKernelGGL(q8_lds_kernel<NWIN>, grid, dim3(576), lds, stream, x, w, row_bytes, y, n, out_feat);
+    return hipGetLastError();
+}
+
+static hipError_t launch_q8_lds(const float* x, const uint8_t* w, size_t row_bytes, float* y, int batch, int n,
+                                int out_feat, hipStream_t stream) {
+    switch (n / 256) {
+#define VTQ_Q8(N) \
+    case N: return launch_q8_lds_n<N>(x, w, row_bytes, y, batch, n, out_feat, stream);
+        VTQ_Q8(1) VTQ_Q8(2) VTQ_Q8(3) VTQ_Q8(4) VTQ_Q8(5) VTQ_Q8(6) VTQ_Q8(7) VTQ_Q8(8)
+        VTQ_Q8(9) VTQ_Q8(10) VTQ_Q8(11) VTQ_Q8(12) VTQ_Q8(13) VTQ_Q8(14) VTQ_Q8(15) VTQ_Q8(16)
+#undef VTQ_Q8
+    }
+    return hipErrorInvalidValue;
+}
+
 template <class Dec>
 static hipError_t launch_pc(const float* x, const uint8_t* w, size_t row_bytes, float* y, int batch, int n,
                             int out_feat, hipStream_t stream) {
@@ -467,7 +663,10 @@ hipError_t launch_canon_gemv(CanonFormat fmt, const float* x, const uint8_t* w, 
     (void)num_cus;
     if (in_feat % 4 == 0) {  // windowed form: x rows stay float4-aligned
         switch (fmt) {
-        case kCanonQ8_0: return launch_pc<DecQ8_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
+        case kCanonQ8_0:
+            if (in_feat % 256 == 0 && in_feat <= 4096)
+                return launch_q8_lds(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
+            return launch_pc<DecQ8_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
         case kCanonQ5_0: return launch_pc<DecQ5_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
         case kCanonQ4_0: return launch_pc<DecQ4_0>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
         case kCanonF32: return launch_pc<DecF32>(x, w, row_bytes, y, batch, in_feat, out_feat, stream);
