@@ -50,7 +50,7 @@ WORKLOADS = {
     "q4k_gemm_prefill": ["q4k_gemm_14336x4096_m512"],
     "e2e_decode": [],  # config 5: libvtq_runtime decode of the random-init 1.1B Llama
 }
-KERNEL_NAME = {12: "kquant_rows_kernel<Q4K>", 14: "kquant_rows_kernel<Q6K>", 8: "canon_pc_kernel<DecQ8_0>"}
+KERNEL_NAME = {12: "kquant_rows_kernel<Q4K>", 14: "kquant_rows_kernel<Q6K>", 8: "q8_lds_kernel<16>"}
 INT8_MFMA_PEAK_TOPS = 5000.0
 
 
