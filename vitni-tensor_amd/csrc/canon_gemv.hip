@@ -457,7 +457,10 @@ typedef __attribute__((address_space(3))) uint8_t lds_u8;
 // such load (vmcnt(0)) before the first barrier or LDS read.  The kernel
 // orders these loads itself with explicit vmcnt waits and barriers; the
 // hardware completes loads in order, so the compiler's own waits on any
-// later load stay correct.
+// later load stay correct.  m0 is a reserved register: the compiler keeps
+// no value of its own in it in these kernels and does not honour it on a
+// clobber list (it only warns), so it is not listed; tests/test_asm_checks.py
+// checks the generated code of every q8_lds_kernel for any other use of m0.
 template <int SIZE>
 __device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t lds_addr) {
     static_assert(SIZE == 16 || SIZE == 4, "dwordx4 or dword");
@@ -465,12 +468,12 @@ __device__ __forceinline__ void load_to_lds(__amdgpu_buffer_rsrc_t rs, uint32_t 
         asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                      :
                      : "v"(voff), "s"(rs), "s"(lds_addr)
-                     : "memory", "m0");
+                     : "memory");
     else
         asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %0, %1, 0 offen lds"
                      :
                      : "v"(voff), "s"(rs), "s"(lds_addr)
-                     : "memory", "m0");
+                     : "memory");
 }
 
 // s_waitcnt vmcnt(N) alone (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt
