@@ -177,6 +177,25 @@ def test_canonical_block_formats(ctx, ggml_type, batch, in_f, out_f):
     check(ctx, ggml_type, 0, x, w, batch, in_f, out_f)
 
 
+# Q8_0 rows of 256..4096 inputs take the LDS-resident kernel, one template
+# instance per 256-element window count; 13 rows leave the second workgroup
+# five of its eight rows, batch 2 runs a second grid slice
+@pytest.mark.parametrize("nwin", range(1, 17))
+@pytest.mark.parametrize("batch,out_f", [(1, 13), (2, 8)])
+def test_q8_0_every_window_count(ctx, nwin, batch, out_f):
+    in_f = 256 * nwin
+    x = synth.activations(batch * in_f, seed=1000 + nwin)
+    check(ctx, vtq.Q8_0, 0, x, synth.weights(vtq.Q8_0, out_f, in_f, seed=2000 + nwin), batch, in_f, out_f)
+
+
+@pytest.mark.parametrize("nwin", [1, 5, 16])
+def test_q8_0_arbitrary_bytes(ctx, nwin):
+    # any bytes: block scales may be Inf, NaN or subnormal f16 values
+    in_f, out_f = 256 * nwin, 11
+    w = O.lcg_bytes(out_f * (in_f // 32) * 34, 0xA5A5 + nwin)
+    check(ctx, vtq.Q8_0, 0, synth.activations(in_f, seed=3000 + nwin), w, 1, in_f, out_f)
+
+
 @pytest.mark.parametrize("batch,in_f,out_f", CANON_SHAPES[:8] + [(1, 13, 4), (1, 4100, 7), (2, 8195, 5)])
 def test_canonical_f32(ctx, batch, in_f, out_f):
     w = synth.weights(vtq.F32, out_f, in_f, seed=in_f * 17 + out_f, sigma=1.0)
