@@ -107,6 +107,14 @@ def test_q4k_prefill_gemm(ctx, batch, in_f, out_f):
     check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
 
 
+# the GEMM walks the batch in launches of 8192 tokens (bounded workspace): one
+# token, and one whole 32-token tile, past the first launch
+@pytest.mark.parametrize("batch,in_f,out_f", [(8193, 256, 40), (8224, 512, 9)])
+def test_q4k_prefill_gemm_batch_chunks(ctx, batch, in_f, out_f):
+    x = synth.activations(batch * in_f, seed=batch)
+    check(ctx, vtq.Q4_K, 0, x, synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f + out_f), batch, in_f, out_f)
+
+
 def test_q4k_prefill_gemm_edge_activations(ctx):
     batch, in_f, out_f = 48, 1024, 40
     x = synth.activations(batch * in_f, seed=5).reshape(batch, in_f)
