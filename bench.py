@@ -386,10 +386,13 @@ def main():
     launch_us = [statistics.median(timer.per_launch_us(lambda k, s, L=L: L.launch(k, s), LAUNCHES_PER_REPLAY,
                                                        args.reps)) for L in lins]
     step_bytes = sum(c.algorithmic_bytes() for c in cfgs)
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    step_ops = sum(2.0 * c.batch * c.out_feat * c.in_feat for c in cfgs)
     dom = max(range(len(cfgs)), key=lambda i: launch_us[i])  # the dominant (slowest) kernel of the step
     dc = cfgs[dom]
     gemm = dc.batch >= 32
+    # GEMV workloads are quoted in GB/s of algorithmic bytes, the prefill GEMM in int8 TOPS
+    value = step_ops / (ms_per_step * 1e-3) / 1e12 if gemm else step_bytes / (ms_per_step * 1e-3) / 1e9
+    value_unit = "TOPS" if gemm else "GB/s"
     if gemm:
         ops = 2.0 * dc.batch * dc.out_feat * dc.in_feat
         achieved, peak, unit = ops / launch_us[dom] / 1e6, INT8_MFMA_PEAK_TOPS, "TOPS"
@@ -407,7 +410,7 @@ def main():
     out = {
         "metric": METRIC,
         "value": round(value, 2),
-        "unit": "GB/s",
+        "unit": value_unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -449,7 +452,8 @@ def main():
 
         sec, n = cpu_time(cpu_step, args.cpu_seconds, min_runs=10)
         out["cpu_baseline"] = {
-            "value": round(step_bytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "value": round(step_ops / sec / 1e12 if gemm else step_bytes / sec / 1e9, 4 if gemm else 3),
+            "unit": value_unit, "cores": threads, "kind": "port",
             "sample": f"full workload, median of {n} steps after 1 warm-up ({sec * 1e3:.1f} ms/step); "
                       f"oracle/vtq_oracle.c row-parallel integer kernels, grain ceil(out/(4*threads)) as "
                       f"src/ops/quant.rs:1171; threads = online cores capped at {CPU_THREAD_CAP}, the GPU box's "
