@@ -64,3 +64,31 @@ def test_q8_lds_kernels_use_m0_only_in_their_lds_loads(canon_asm):
             n_loads += 1
         assert n_loads > 0, name
 
+
+
+def _scratch_sizes(src):
+    """{kernel symbol: private segment bytes per lane} of one source file."""
+    out = subprocess.run([HIPCC if os.path.exists(HIPCC) else "hipcc", *FLAGS, "--cuda-device-only", "-S", "-o", "-",
+                          src], check=True, stdout=subprocess.PIPE, stderr=subprocess.DEVNULL, timeout=600).stdout
+    sizes, cur = {}, None
+    for line in out.decode().split("\n"):
+        m = re.match(r"^([_A-Za-z][\w.$]*):", line)
+        if m and not line.startswith(".L"):
+            cur = m.group(1)
+        m = re.match(r"^; ScratchSize: (\d+)", line.strip())
+        if m and cur:
+            sizes[cur] = int(m.group(1))
+    return sizes
+
+
+@pytest.mark.parametrize("name", ["kquant_gemv.hip", "canon_gemv.hip"])
+def test_gemv_kernels_do_not_spill(name):
+    # a value spilled to scratch memory is reloaded through the memory
+    # hierarchy; in the GEMVs such a reload sat on the critical path
+    if not (os.path.exists(HIPCC) or shutil.which("hipcc")):
+        pytest.skip("hipcc not available")
+    sizes = _scratch_sizes(os.path.join(ROOT, "vitni-tensor_amd", "csrc", name))
+    kernels = {k: v for k, v in sizes.items() if "kernel" in k}
+    assert kernels, name
+    spilled = {k: v for k, v in kernels.items() if v}
+    assert not spilled, spilled

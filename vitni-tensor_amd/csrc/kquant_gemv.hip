@@ -541,8 +541,14 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
     __syncthreads();
 
     typename Fmt::X xr[NWIN];
+    // the block slot once more from the thread index, through an opaque copy:
+    // held from the top across the normalising chain, it was spilled to
+    // scratch memory and reloaded here
+    int tid_late = (int)threadIdx.x;
+    asm volatile("" : "+v"(tid_late));
+    const int gl = HALF ? ((tid_late >> 2) & 7) : ((tid_late & 63) >> 2);
 #pragma unroll
-    for (int w = 0; w < NWIN; w++) Fmt::load_x(xr[w], act, 16 * w + g < R ? 16 * w + g : R - 1, k);
+    for (int w = 0; w < NWIN; w++) Fmt::load_x(xr[w], act, 16 * w + gl < R ? 16 * w + gl : R - 1, k);
     const typename Fmt::Lane lc = Fmt::lane_consts(k);
     if constexpr (PREW > 0) load_row(buf[0], 0, PREW, NWIN);
     if constexpr (!POSTX) {
