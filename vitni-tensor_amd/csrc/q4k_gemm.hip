@@ -61,28 +61,31 @@ inline GemmWs gemm_ws(void* base, int Mp, int R) {
 
 // quantize_block_q8 (src/ops/quant.rs:750-771) of every 256-block of every
 // batch row: one wave per (token, super-block), written in the tiled layout.
-__global__ __launch_bounds__(256) void act_quant_tiles_kernel(const float* __restrict__ x, GemmWs ws, int R, int M,
-                                                              int Mp) {
+// Workgroup (s, q) holds the 16 consecutive tokens 16q..16q+15 of
+// super-block s, so each 256-byte run of the token operands (and the 16
+// d / bsum entries beside it) is written by one workgroup at once.
+constexpr int kQuantWaves = 16;
+__global__ __launch_bounds__(kQuantWaves * 64) void act_quant_tiles_kernel(const float* __restrict__ x, GemmWs ws,
+                                                                           int R, int M) {
     const int lane = threadIdx.x & 63;
-    const long blk = (long)blockIdx.x * 4 + wave_id();
-    if (blk >= (long)Mp * R) return;
-    const long b = blk / R, s = blk % R;
-    const long tile = (b >> 5) * R + s;
-    const int n = (int)(b & 31);
+    const int s = (int)blockIdx.x;
+    const int b = (int)blockIdx.y * kQuantWaves + wave_id();  // < Mp: the grid covers Mp / 16 groups
+    const int tile = (b >> 5) * R + s;
+    const int n = b & 31;
     uint32_t packed = 0;
     int s16 = 0, s32 = 0;
     float d = 0.0f;
     if (b < M) {  // uniform per wave
-        const float4 v = reinterpret_cast<const float4*>(x + b * (long)R * 256 + s * 256)[lane];
+        const float4 v = reinterpret_cast<const float4*>(x + (size_t)b * R * 256 + (size_t)s * 256)[lane];
         d = quant_block_wave(v, &packed, &s16, &s32);
     }
     // lane holds elements 4*lane .. +3: k-step j = lane/8, half g = (lane/4)&1
     const int j = lane >> 3, g = (lane >> 2) & 1;
-    uint8_t* dst = reinterpret_cast<uint8_t*>(ws.xqt + (tile * 8 + j) * 64 + 32 * g + n) + 4 * (lane & 3);
+    uint8_t* dst = reinterpret_cast<uint8_t*>(ws.xqt + ((size_t)tile * 8 + j) * 64 + 32 * g + n) + 4 * (lane & 3);
     *reinterpret_cast<uint32_t*>(dst) = packed;
-    if (lane == 0) ws.xdt[tile * 32 + n] = d;
+    if (lane == 0) ws.xdt[(size_t)tile * 32 + n] = d;
     if ((lane & 7) == 0) {
-        int8_t* o = reinterpret_cast<int8_t*>(ws.xbt + tile * 32 + n);
+        int8_t* o = reinterpret_cast<int8_t*>(ws.xbt + (size_t)tile * 32 + n);
         o[j] = (int8_t)(s32 & 63);      // bl
         o[8 + j] = (int8_t)(s32 >> 6);  // bh (arithmetic shift: s32 = 64*bh + bl)
     }
@@ -321,9 +324,9 @@ hipError_t launch_q4k_gemm(const float* x, const uint8_t* w, float* y, int batch
     for (int b0 = 0; b0 < batch; b0 += kChunkM) {
         const int M = min(batch - b0, kChunkM), Mp = (M + 31) / 32 * 32;
         const GemmWs ws = gemm_ws(workspace, Mp, R);
-        const long blocks = (long)Mp * R;
-        hipLaunchKernelGGL(act_quant_tiles_kernel, dim3((unsigned)((blocks + 3) / 4)), dim3(256), 0, stream,
-                           x + (size_t)b0 * in_feat, ws, R, M, Mp);
+        // Mp is a multiple of 32, so Mp / 16 groups cover every token slot
+        hipLaunchKernelGGL(act_quant_tiles_kernel, dim3((unsigned)R, (unsigned)(Mp / kQuantWaves)),
+                           dim3(kQuantWaves * 64), 0, stream, x + (size_t)b0 * in_feat, ws, R, M);
         if (hipError_t e = hipGetLastError()) return e;
         const int TT = (M + kTB - 1) / kTB;
         const dim3 grid((unsigned)NR * (unsigned)TT);
