@@ -35,6 +35,7 @@
 #include "vtq_device.h"
 #include "vtq_kernels.h"
 #include "vtq_libm.h"
+#include "vtq_sumsq.h"
 
 #include <type_traits>
 
@@ -75,6 +76,8 @@ constexpr int kNW = 16;        // waves per workgroup; one workgroup per CU
 constexpr int kXPerWave = 4;   // activation blocks each wave loads up front (R <= 64 fully overlapped)
 __host__ __device__ constexpr size_t act_lds_end(int R) { return act_off_ws(R) + kNW * kMaxWindows * 4; }
 size_t act_lds_bytes(int R) { return act_lds_end(R); }
+// the sum-of-squares walk's tables: past the products (npass x 16 KiB) and the scale
+__host__ __device__ constexpr size_t norm_walk_off(int R) { return act_lds_end(R) + (size_t)(R + 15) / 16 * 16384 + 16; }
 
 // quantize_block_q8 (src/ops/quant.rs:750-771) of 256-block b, held as one
 // float4 per lane (elements 4L..4L+3), into the LDS activation arrays.
@@ -498,25 +501,44 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
         __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (NORM) {
-        // rms_norm_slice: x*x per element into LDS past the activation arrays,
-        // the sum of squares serially by wave 0 (serial_sum_lanes over passes
-        // of 16 blocks: in pass P, element 64L + k of the pass sits at float
-        // 4096P + 256(k/4) + 4L + k%4, so lane L reads its 64 values as
-        // sixteen conflict-free float4), then x * scale * w
+        // rms_norm_slice: x*x per element into LDS past the activation arrays
+        // (in pass P, element 64L + k of the pass sits at float 4096P +
+        // 256(k/4) + 4L + k%4, so lane L reads its 64 values as sixteen
+        // conflict-free float4), the sum of squares in the reference's serial
+        // order (by wave 0, with the walk of vtq_sumsq.h where it applies),
+        // then x * scale * w
         float* prod = reinterpret_cast<float*>(lds + act_lds_end(R));
         const int npass = (R + 15) / 16;
+        const int H = sumsq_walk_head(R * 256);  // 0: the plain chain only (uniform)
+        SumsqWalk& walk = *reinterpret_cast<SumsqWalk*>(lds + norm_walk_off(R));
+        float hpart = 0.0f, apart = 0.0f;
 #pragma unroll
         for (int j = 0; j < NWIN; j++) {
             const int b = wave + kNW * j;
             const float4 v = xv[j];
+            const float4 sq = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
             // elements 256b + 4 lane + c: pass b/16, segment 4(b%16) + lane/16, k = 4(lane%16) + c
-            if (b < R)
-                reinterpret_cast<float4*>(prod + 4096 * (b >> 4) + 256 * (lane & 15) + 16 * (b & 15))[lane >> 4] =
-                    make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+            if (b < R) {
+                reinterpret_cast<float4*>(prod + 4096 * (b >> 4) + 256 * (lane & 15) + 16 * (b & 15))[lane >> 4] = sq;
+                const float s4 = (sq.x + sq.y) + (sq.z + sq.w);
+                apart += s4;
+                if (256 * b + 4 * lane < H) hpart += s4;  // H is a multiple of 64
+            }
         }
+        if (H) sumsq_walk_partials(hpart, apart, walk);
         __syncthreads();
-        if (wave == 0) {
-            float sumsq = 0.0f;
+        float sumsq = 0.0f;
+        if (H) {
+            if (wave == 0) {
+                float r[64];
+                sumsq_load_pass0(prod, r);
+                sumsq = sumsq_chain(r, 0, H / 64, 0.0f);
+            } else if (wave < 4) {
+                sumsq_walk_helper(wave - 1, prod, R * 256, H, walk);  // waves 1-3: the other three SIMDs
+            }
+            __syncthreads();
+            if (wave == 0) sumsq = sumsq_walk(sumsq, prod, R * 256, H, walk);
+        } else if (wave == 0) {
             for (int ps = 0; ps < npass; ps++) {
                 float r[64];
 #pragma unroll
@@ -526,6 +548,8 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
                 }
                 sumsq = serial_sum_lanes(r, 4 * min(16, R - 16 * ps), sumsq);
             }
+        }
+        if (wave == 0) {
             const float mean = sumsq / (float)(R * 256);
             if (lane == 0) prod[4096 * npass] = 1.0f / libm::sqrtf(mean + args.eps);
         }
@@ -728,8 +752,11 @@ template <class K, class... A>
 static hipError_t launch(K kern, int wgs, int batch, int R, hipStream_t stream, A... a) {
     return launch_lds(kern, wgs, batch, act_lds_bytes(R), stream, a...);
 }
-// the normalising prologue keeps the products (passes of 2048 floats) and the scale past the activation arrays
-static size_t norm_lds_bytes(int R) { return act_lds_bytes(R) + (size_t)(R + 15) / 16 * 16384 + 16; }
+// the normalising prologue keeps the products (passes of 4096 floats), the
+// scale and, where the walk applies, its tables past the activation arrays
+static size_t norm_lds_bytes(int R) {
+    return norm_walk_off(R) + (sumsq_walk_head(R * 256) ? sizeof(SumsqWalk) : 0);
+}
 
 // one 16-wave workgroup per CU; more if a wave would own over 64 rows
 static int rows_grid(int out_feat, int num_cus) {

@@ -13,6 +13,7 @@
 #include "vtq_device.h"
 #include "vtq_kernels.h"
 #include "vtq_libm.h"
+#include "vtq_sumsq.h"
 
 namespace vtq {
 namespace decode {
@@ -114,18 +115,51 @@ __global__ __launch_bounds__(256) void embed_kernel(int type, const uint8_t* __r
     for (int i = threadIdx.x; i < dim; i += blockDim.x) x[i] = embed_elem(type, row, i);
 }
 
-// products in parallel, the sum of squares serially by wave 0
+// products in parallel, the sum of squares in the reference's serial order
+// by wave 0: where the walk of vtq_sumsq.h applies (1024-4096 terms, a
+// multiple of 64) with the products in its pass layout and waves 1-3 as its
+// helpers, otherwise as one chain over the products in order
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int n,
                                                        float eps, float* __restrict__ out) {
     extern __shared__ float4 prod4[];
     float* prod = reinterpret_cast<float*>(prod4);
     __shared__ float scale_s;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) prod[i] = x[i] * x[i];
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        const float sumsq = serial_sum_wave(prod, n);
-        const float mean = sumsq / (float)n;
-        if (threadIdx.x == 0) scale_s = 1.0f / libm::sqrtf(mean + eps);
+    const int H = sumsq_walk_head(n);  // uniform
+    if (H) {
+        const int wave = threadIdx.x >> 6;
+        SumsqWalk& walk = *reinterpret_cast<SumsqWalk*>(prod + 4096);
+        float hpart = 0.0f, apart = 0.0f;
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const float p = x[i] * x[i];
+            prod[sumsq_pass_index(i)] = p;
+            apart += p;
+            if (i < H) hpart += p;
+        }
+        if (threadIdx.x < 32 && (threadIdx.x & 15) >= 4) walk.part[threadIdx.x >> 4][threadIdx.x & 15] = 0.0f;  // no waves 4-15
+        sumsq_walk_partials(hpart, apart, walk);
+        __syncthreads();
+        float sumsq = 0.0f;
+        if (wave == 0) {
+            float r[64];
+            sumsq_load_pass0(prod, r);
+            sumsq = sumsq_chain(r, 0, H / 64, 0.0f);
+        } else {
+            sumsq_walk_helper(wave - 1, prod, n, H, walk);
+        }
+        __syncthreads();
+        if (wave == 0) {
+            sumsq = sumsq_walk(sumsq, prod, n, H, walk);
+            const float mean = sumsq / (float)n;
+            if (threadIdx.x == 0) scale_s = 1.0f / libm::sqrtf(mean + eps);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n; i += blockDim.x) prod[i] = x[i] * x[i];
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            const float sumsq = serial_sum_wave(prod, n);
+            const float mean = sumsq / (float)n;
+            if (threadIdx.x == 0) scale_s = 1.0f / libm::sqrtf(mean + eps);
+        }
     }
     __syncthreads();
     const float scale = scale_s;
@@ -472,7 +506,9 @@ hipError_t embed(int ggml_type, const uint8_t* table, uint32_t rows, const uint3
 }
 
 hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out, hipStream_t stream) {
-    const size_t lds = (size_t)((n + 3) & ~3) * 4;  // the serial sum reads whole float4s
+    // the walk: one 4096-float pass of products and its tables; else the
+    // products in order (the serial sum reads whole float4s)
+    const size_t lds = sumsq_walk_head(n) ? 4096 * 4 + sizeof(SumsqWalk) : (size_t)((n + 3) & ~3) * 4;
     if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(rms_norm_kernel), lds)) return e;
     hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(256), lds, stream, x, w, n, eps, out);
     return hipGetLastError();
