@@ -49,7 +49,7 @@ constexpr uint32_t kWalkCap = 1u << 25;
 // Length of the serial head for n terms, or 0 where the walk does not apply
 // (n not a multiple of 64, below 1024 or above 4096 terms).
 __host__ __device__ constexpr int sumsq_walk_head(int n) {
-    return (n % 64 == 0 && n >= 1024 && n <= 4096) ? (n - kWalkMaxTerms > 768 ? n - kWalkMaxTerms : 768) : 0;
+    return (n % 64 == 0 && n >= 1024 && n <= 4096) ? (n - kWalkMaxTerms > 640 ? n - kWalkMaxTerms : 640) : 0;
 }
 
 struct SumsqWalk {
