@@ -22,6 +22,13 @@ MEDIUM = dict(dim=512, hidden=1536, layers=4, heads=8, kv_heads=2, vocab=4096, c
 # hidden 4352: two-window rows for W2
 WIDE = dict(dim=2560, hidden=4352, layers=1, heads=20, kv_heads=4, vocab=512, ctx=300, rope_theta=10000.0,
             rms_eps=1e-5)
+# dim 1024 and 4096: the smallest and largest rows the fused RMSNorm's binade
+# walk takes (a 640-term serial head, and a 2560-term one with the walk's full
+# 1536 terms after it)
+WALK_LO = dict(dim=1024, hidden=768, layers=1, heads=16, kv_heads=4, vocab=512, ctx=40, rope_theta=10000.0,
+               rms_eps=1e-5)
+WALK_HI = dict(dim=4096, hidden=1024, layers=1, heads=32, kv_heads=8, vocab=512, ctx=40, rope_theta=10000.0,
+               rms_eps=1e-5)
 
 
 def compare(cfg, prompt_len, n_new, regimes=(0, 1), threads=8, **variant):
@@ -59,6 +66,11 @@ def test_e2e_medium_odd_lengths():
 
 def test_e2e_wide_long_context():
     compare(WIDE, 250, 12, regimes=(0,), threads=16)
+
+
+def test_e2e_walk_row_bounds():
+    compare(WALK_LO, 5, 9, regimes=(0,))
+    compare(WALK_HI, 5, 9, regimes=(0,), threads=16)
 
 
 def test_e2e_qwen2_neox_bias_tied_head():

@@ -2,7 +2,9 @@
 
 The sum of squares is the reference's serial fp32 chain (src/ops/rms_norm.rs:
 60-110), which the GPU runs as a register chain with readlane hand-offs
-between 32-value segments.  The inputs cover round-to-even ties (short
+between 32-value segments, or, for 1024-4096 values (a multiple of 64), as a
+serial head followed by an exact walk over per-binade integer prefix sums
+(the sizes around 1024, 2048 and 4096 take both forms).  The inputs cover round-to-even ties (short
 mantissas, small half-integers), subnormal squares, a sum that overflows to
 inf, NaN, zero runs, binade changes late in the chain, and sizes around the
 segment and 2048-value pass boundaries.  Outputs must match bit for bit (NaN
@@ -19,7 +21,8 @@ pytestmark = pytest.mark.gpu
 
 # up to 32768, the entry point's limit; past 16384 the products take more
 # than 64 KiB of LDS (the kernel's raised dynamic-LDS limit)
-SIZES = [1, 7, 256, 575, 576, 1000, 2048, 2049, 2560, 4096, 4607, 4608, 4609, 5000, 8192, 16384, 16385, 32768]
+SIZES = [1, 7, 256, 575, 576, 1000, 1024, 1040, 1088, 2048, 2049, 2112, 2560, 3072, 4032, 4096, 4160, 4607, 4608,
+         4609, 5000, 8192, 16384, 16385, 32768]
 
 
 def make_x(kind, n, rng):
