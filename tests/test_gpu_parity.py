@@ -107,6 +107,58 @@ def test_q4k_prefill_gemm(ctx, batch, in_f, out_f):
     check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
 
 
+# rows of at most 16 super-blocks take the per-wave GEMM (32 rows x 64 tokens
+# per wave, 128-row workgroups): every row length 1..16 (each tree shape of
+# its counter), token counts either side of the 32- and 64-token tiles, row
+# counts either side of the 32-row tiles and the 128-row workgroups
+PW_SHAPES = [(32, 256, 129), (64, 512, 1), (33, 768, 129), (65, 1024, 300), (96, 1280, 128), (97, 1536, 513),
+             (127, 1792, 31), (128, 2048, 130), (34, 2304, 64), (200, 2560, 257), (70, 2816, 77),
+             (160, 3072, 96), (129, 3328, 33), (95, 3584, 200), (63, 3840, 127), (192, 4096, 255)]
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", PW_SHAPES)
+def test_q4k_prefill_gemm_per_wave_shapes(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 13 + out_f)
+    x = synth.activations(batch * in_f, seed=in_f * 17 + batch)
+    check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
+
+
+def q4k_blocks(rows, in_f, d_bits, dmin_bits, scale_byte, seed):
+    """Q4_K blocks with fixed f16 d / dmin and all twelve scale bytes equal
+    (0xFF: every sub-block scale and min is 63; 0x00: all 0), random codes."""
+    w = O.lcg_bytes(rows * (in_f // 256) * 144, seed).reshape(-1, 144)
+    w[:, 0:2] = np.frombuffer(np.uint16(d_bits).tobytes(), np.uint8)
+    w[:, 2:4] = np.frombuffer(np.uint16(dmin_bits).tobytes(), np.uint8)
+    w[:, 4:16] = scale_byte
+    return w.reshape(-1)
+
+
+def test_q4k_prefill_gemm_min_term_extremes(ctx):
+    # the per-wave GEMM forms the min term sum_j m_j * bsum_j on an f16 MFMA:
+    # m = 63 with |bsum| = 4064 (every code +-127) gives the largest |accm|
+    # (2,048,256), and alternating signs per sub-block give partial sums of
+    # both signs
+    batch, in_f, out_f = 64, 4096, 64
+    x = np.ones((batch, in_f), F)
+    x[1::2] = -1.0
+    x[2::4] *= np.repeat(np.array([1, -1] * (in_f // 64), F), 32)
+    x[3::4] = synth.activations(in_f * (batch // 4), seed=11).reshape(batch // 4, in_f)
+    w = q4k_blocks(out_f, in_f, 0x2E66, 0x2666, 0xFF, 0xAB)
+    check(ctx, vtq.Q4_K, 0, x.reshape(-1), w, batch, in_f, out_f)
+
+
+def test_q4k_prefill_gemm_zero_min_sign(ctx):
+    # m = 0 against negative bsums makes every min-term product -0.0; the
+    # reference's f32(accm = 0) is +0.0, so the sum must come out +0.0.  With
+    # sc = 0, d < 0 and dmin > 0 every part is (-0.0) - (+0.0) = -0.0 and the
+    # outputs are -0.0; a -0.0 min term would turn them into +0.0.
+    batch, in_f, out_f = 64, 2048, 40
+    x = -np.abs(synth.activations(batch * in_f, seed=21))
+    w = q4k_blocks(out_f, in_f, 0xBC00, 0x3C00, 0x00, 0xCD)  # d = -1.0, dmin = +1.0
+    got = check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
+    assert np.all(got.view(np.uint32) == np.uint32(0x80000000))
+
+
 # the GEMM walks the batch in launches of 8192 tokens (bounded workspace): one
 # token, and one whole 32-token tile, past the first launch
 @pytest.mark.parametrize("batch,in_f,out_f", [(8193, 256, 40), (8224, 512, 9)])

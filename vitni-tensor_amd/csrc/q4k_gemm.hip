@@ -6,23 +6,27 @@
 //   accm = sum_j m_j  * bsum_j
 //   part = (d*dx) * f32(acc) - (dmin*dx) * f32(accm)
 //
-// Integer work on v_mfma_i32_32x32x32_i8:
+// Integer work on the matrix cores:
 //  * the 6-bit sub-block scale is folded into the weight operand by a 3+3 bit
 //    split, sc = 8*sh + sl: A1 = q*sh and A0 = q*sl are both <= 105 (i8), and
 //    acc = 8*C1 + C0 exactly (|C1| <= 256*105*127), so one super-block is 16
-//    MFMAs whose accumulators run over all 256 elements;
-//  * the min term is one more pair of MFMAs over the 8 sub-blocks with
-//    bsum = 64*bh + bl split into two i8 operands (bl in [0,63], bh in [-64,63]);
-//    accm = 64*Ch + Cl exactly.
+//    v_mfma_i32_32x32x32_i8 whose accumulators run over all 256 elements;
+//  * the min term pairs m_j with bsum_j = 64*bh_j + bl_j: two i8 MFMAs and
+//    accm = 64*Ch + Cl in the LDS-operand kernel, one f16 MFMA in the
+//    per-wave kernel (see there why that is exact).
 // Integer sums are exact in any order, so the MFMA reduction order is free.
 // The float epilogue is the reference's, per (b, o, s), in VALU, and the
-// fixed_tree over super-blocks is kept in registers as a binary counter:
+// fixed_tree over super-blocks is a streamed binary counter:
 // fixed_tree(p[0..R)) == fold-right over the balanced trees of the binary
 // digits of R, each built left to right as parts arrive.
 //
-// Tile: a workgroup of 4 waves owns 32 weight rows x 128 tokens; wave w owns
-// tokens 32w..32w+31 of the tile.  The activation pre-pass writes the token
-// codes in the MFMA operand order, so each wave's operand loads are contiguous.
+// Two kernels share the activation pre-pass, which writes the token codes in
+// the MFMA operand order:
+//  * q4k_gemm_pw_kernel (rows of at most 16 super-blocks, in_feat <= 4096):
+//    each wave forms its own weight operands in registers, no barriers;
+//  * q4k_gemm_kernel (longer rows): a workgroup of 4 waves owns 32 weight
+//    rows x 128 tokens and builds the weight operands once per super-block
+//    in LDS.
 #include "vtq_device.h"
 #include "vtq_kernels.h"
 
@@ -39,12 +43,20 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 //                                   of token 32T+n (the MFMA B operand, so one
 //                                   wave reads 1 KB contiguous per k-step)
 //   xdt [Mp/32][R][32] f32          d of each (token, super-block)
-//   xbt [Mp/32][R][32] x 16 B       bl[8] = bsum & 63, bh[8] = bsum >> 6
+// and one min-term operand, whichever the launch's GEMM kernel reads (the two
+// share their space):
+//   xbt [Mp/32][R][32] x 16 B       bl[8] = bsum & 63, bh[8] = bsum >> 6 (i8)
+//   xmt [Mp/32][R][64] x 16 B       lane n: f16(64*bh_0..7) of token 32T+n,
+//                                   lane 32+n: f16(bl_0..7)
 struct GemmWs {
     v4i* xqt;
     float* xdt;
     v4i* xbt;
+    v4i* xmt;
 };
+
+// Descriptor word 3 of a raw (untyped, stride 0) buffer on gfx9-family parts.
+constexpr int kGemmWord3 = 0x00020000;
 
 inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
@@ -56,6 +68,7 @@ inline GemmWs gemm_ws(void* base, int Mp, int R) {
     w.xdt = reinterpret_cast<float*>(p);
     p += align256((size_t)Mp * R * 4);
     w.xbt = reinterpret_cast<v4i*>(p);
+    w.xmt = reinterpret_cast<v4i*>(p);
     return w;
 }
 
@@ -66,7 +79,7 @@ inline GemmWs gemm_ws(void* base, int Mp, int R) {
 // d / bsum entries beside it) is written by one workgroup at once.
 constexpr int kQuantWaves = 16;
 __global__ __launch_bounds__(kQuantWaves * 64) void act_quant_tiles_kernel(const float* __restrict__ x, GemmWs ws,
-                                                                           int R, int M) {
+                                                                           int R, int M, int f16_min) {
     const int lane = threadIdx.x & 63;
     const int s = (int)blockIdx.x;
     const int b = (int)blockIdx.y * kQuantWaves + wave_id();  // < Mp: the grid covers Mp / 16 groups
@@ -85,9 +98,16 @@ __global__ __launch_bounds__(kQuantWaves * 64) void act_quant_tiles_kernel(const
     *reinterpret_cast<uint32_t*>(dst) = packed;
     if (lane == 0) ws.xdt[(size_t)tile * 32 + n] = d;
     if ((lane & 7) == 0) {
-        int8_t* o = reinterpret_cast<int8_t*>(ws.xbt + (size_t)tile * 32 + n);
-        o[j] = (int8_t)(s32 & 63);      // bl
-        o[8 + j] = (int8_t)(s32 >> 6);  // bh (arithmetic shift: s32 = 64*bh + bl)
+        if (f16_min) {
+            // exact in f16: |64*bh| <= 4096 is a multiple of 64, 0 <= bl <= 63
+            _Float16* o = reinterpret_cast<_Float16*>(ws.xmt + (size_t)tile * 64 + n);
+            o[j] = (_Float16)(float)(s32 - (s32 & 63));  // 64*bh
+            o[32 * 8 + j] = (_Float16)(float)(s32 & 63);  // bl, lane 32 + n
+        } else {
+            int8_t* o = reinterpret_cast<int8_t*>(ws.xbt + (size_t)tile * 32 + n);
+            o[j] = (int8_t)(s32 & 63);      // bl
+            o[8 + j] = (int8_t)(s32 >> 6);  // bh (arithmetic shift: s32 = 64*bh + bl)
+        }
     }
 }
 
@@ -300,10 +320,281 @@ __global__ __launch_bounds__(256, 2) void q4k_gemm_kernel(const uint8_t* __restr
     }
 }
 
+// ------------------------------------------- per-wave operand formation
+
+// Rows of at most 16 super-blocks (in_feat <= 4096).  Each wave owns 32
+// weight rows x 64 tokens (two 32-token tiles) and forms the split weight
+// operands of its rows in registers, straight from the 144-byte blocks: no
+// LDS operand buffers and no workgroup barrier, so the two waves sharing a
+// SIMD drift out of phase and one's MFMAs run beside the other's epilogue.
+// One formed operand feeds the MFMAs of both tiles.
+//
+// A workgroup is four waves on four consecutive 32-row tiles and the same 64
+// tokens, so the token operands of a super-block are fetched from L2 once per
+// workgroup and the other three waves can hit L1.  Every operand load is a
+// raw buffer load whose per-lane part is a fixed register and whose per-step
+// part is a scalar offset, so the loop spends no vector instructions on
+// addresses.  The token operands run in a ring of four k-steps.
+//
+// The min term runs on one v_mfma_f32_32x32x16_f16: k 0..7 pair m_j with
+// 64*bh_j, k 8..15 pair m_j with bl_j (bsum_j = 64*bh_j + bl_j).  Every
+// operand is an integer that f16 holds exactly (m <= 63, |64*bh| <= 4096,
+// bl <= 63), every product is exact in f32, and every partial sum is an
+// integer below 2^22 in magnitude, so the f32 result is accm exactly, the
+// value f32(accm) of the reference (|accm| < 2^24).  The accumulator input
+// is +0.0, so a sum with no nonzero term is +0.0, as f32(0) is.
+//
+// fixed_tree as a binary counter: levels 0 and 1 in registers, levels 2 and
+// 3 in the wave's own LDS (each written and read a few times per row); at
+// the last super-block the counter folds straight into the result, so level
+// 4 (R = 16) is never stored.
+constexpr int kPwWaves = 4;
+constexpr int kPwLevelBytes = 2 * 4 * 64 * 16;                 // one tree level of both tiles
+constexpr int kPwLdsPerWave = 2 * kPwLevelBytes + 2 * 32 * 4;  // levels 2 and 3, then d and dmin of the rows
+constexpr int kPwMaxR = 16;
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ uint32_t rep_byte16(uint32_t v, int j) {
+    // byte j of v into both 16-bit halves: {b_j, 0, b_j, 0}
+    return __builtin_amdgcn_perm(0u, v, (uint32_t)j | 0x0C000C00u | ((uint32_t)j << 16));
+}
+__device__ __forceinline__ v4i bload16(__amdgpu_buffer_rsrc_t rs, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+}
+__device__ __forceinline__ uint32_t pk_f16(uint32_t a, uint32_t b) {  // two small integers as packed f16 (exact)
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz((float)a, (float)b));
+}
+
+__global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uint8_t* __restrict__ W, GemmWs ws,
+                                                                       float* __restrict__ y, int R, int N, int M,
+                                                                       int NG, int TP) {
+    constexpr int NT = 2, D = 4, NW = kPwWaves;  // tiles per wave, k-steps of token operands in flight
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    float4* lv = reinterpret_cast<float4*>(lds + (size_t)wave * kPwLdsPerWave);  // [level 2..3][tile][q][lane]
+    float* dd = reinterpret_cast<float*>(lds + (size_t)wave * kPwLdsPerWave + 2 * kPwLevelBytes);  // d[32], dmin[32]
+
+    // Workgroup i runs on XCD i % 8: the TP token groups of one 128-row group
+    // get consecutive slots of one XCD, so its weights stream into one L2.
+    const int id = blockIdx.x, full = (NG / 8) * 8 * TP;
+    int rg, tp;
+    if (id < full) {
+        const int k = id >> 3;
+        rg = (k / TP) * 8 + (id & 7);
+        tp = k % TP;
+    } else {
+        rg = (NG / 8) * 8 + (id - full) / TP;
+        tp = (id - full) % TP;
+    }
+    const int o0 = (rg * NW + wave) * 32;
+    const int r = lane & 31, g = lane >> 5;
+    const int Mt = (M + 31) / 32;
+
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(ws.xqt, (short)0, Mt * R * 8192, kGemmWord3);
+    const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(ws.xmt, (short)0, Mt * R * 1024, kGemmWord3);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(ws.xdt, (short)0, Mt * R * 128, kGemmWord3);
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), (short)0, N * R * 144, kGemmWord3);
+    uint32_t q0[NT], m0[NT], d0[NT];  // tile bases (scalar); past the end a tile recomputes the last one
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const uint32_t T = (uint32_t)min(NT * tp + t, Mt - 1);
+        q0[t] = T * R * 8192;
+        m0[t] = T * R * 1024;
+        d0[t] = T * R * 128;
+    }
+    const uint32_t vq = 16u * lane, vd = 4u * r;
+    // lane (r, g): header of row r, and code bytes 32h + 16g .. +15 of each
+    // quarter h: low nibbles are k-step 2h, high nibbles k-step 2h + 1, both
+    // at k = 16g .. 16g + 15 of the step (the B operand's order)
+    const uint32_t vh = (uint32_t)min(o0 + r, N - 1) * ((uint32_t)R * 144), vc = vh + 16 + 16 * g;
+
+    uint4 hdr = __builtin_bit_cast(uint4, bload16(rw, vh, 0));
+    uint4 qw[4];
+#pragma unroll
+    for (int h = 0; h < 4; h++) qw[h] = __builtin_bit_cast(uint4, bload16(rw, vc + 32 * h, 0));
+    v4i bq[NT][D];  // token operands: ring of D k-steps
+#pragma unroll
+    for (int j = 0; j < D; j++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) bq[t][j] = bload16(rq, vq, q0[t] + j * 1024);
+    v4i bm[NT];
+    float dx[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        bm[t] = bload16(rm, vq, m0[t]);
+        dx[t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rd, vd, d0[t], 0));
+    }
+
+    float L0[NT][16], L1[NT][16];
+
+    // one super-block: the parts of every tile into p
+    auto sblock = [&](int s, float (&p)[NT][16]) __attribute__((always_inline)) {
+        const int sn = min(s + 1, R - 1);
+        // get_scale_min_k4 (src/ops/quant.rs:267-276) of all eight sub-blocks, a byte each
+        const uint32_t Y = hdr.y, Z = hdr.z, Wd = hdr.w;
+        const uint32_t SCl = Y & 0x3F3F3F3Fu, Ml = Z & 0x3F3F3F3Fu;
+        const uint32_t SCh = (Wd & 0x0F0F0F0Fu) | ((Y >> 2) & 0x30303030u);
+        const uint32_t Mh = ((Wd >> 4) & 0x0F0F0F0Fu) | ((Z >> 2) & 0x30303030u);
+        const uint32_t SHl = (SCl >> 3) & 0x07070707u, SLl = SCl & 0x07070707u;
+        const uint32_t SHh = (SCh >> 3) & 0x07070707u, SLh = SCh & 0x07070707u;
+        if (g == 0) {
+            dd[r] = f16_to_f32_sel(hdr.x & 0xFFFFu);
+            dd[32 + r] = f16_to_f32_sel(hdr.x >> 16);
+        }
+        const uint32_t am0 = pk_f16(Ml & 255u, (Ml >> 8) & 255u), am1 = pk_f16((Ml >> 16) & 255u, Ml >> 24);
+        const uint32_t am2 = pk_f16(Mh & 255u, (Mh >> 8) & 255u), am3 = pk_f16((Mh >> 16) & 255u, Mh >> 24);
+        const v8h am = __builtin_bit_cast(v8h, v4i{(int)am0, (int)am1, (int)am2, (int)am3});
+        hdr = __builtin_bit_cast(uint4, bload16(rw, vh, (uint32_t)sn * 144));
+        v16i c1[NT], c0[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) c1[t] = c0[t] = v16i{};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int h = j >> 1, sh = 4 * (j & 1);
+            const uint32_t SH = j < 4 ? SHl : SHh, SL = j < 4 ? SLl : SLh;
+            const us2 mh = __builtin_bit_cast(us2, rep_byte16(SH, j & 3));
+            const us2 ml = __builtin_bit_cast(us2, rep_byte16(SL, j & 3));
+            const uint32_t w0 = (qw[h].x >> sh) & 0x0F0F0F0Fu, w1 = (qw[h].y >> sh) & 0x0F0F0F0Fu;
+            const uint32_t w2 = (qw[h].z >> sh) & 0x0F0F0F0Fu, w3 = (qw[h].w >> sh) & 0x0F0F0F0Fu;
+            const v4i a1 = v4i{nib_mul(w0, mh), nib_mul(w1, mh), nib_mul(w2, mh), nib_mul(w3, mh)};
+            const v4i a0 = v4i{nib_mul(w0, ml), nib_mul(w1, ml), nib_mul(w2, ml), nib_mul(w3, ml)};
+            if (j & 1) qw[h] = __builtin_bit_cast(uint4, bload16(rw, vc + 32 * h, (uint32_t)sn * 144));
+#pragma unroll
+            for (int t = 0; t < NT; t++) c1[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, bq[t][j % D], c1[t], 0, 0, 0);
+#pragma unroll
+            for (int t = 0; t < NT; t++) c0[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, bq[t][j % D], c0[t], 0, 0, 0);
+            // refill the ring slot: k-step j + D of this super-block, or of the next
+            const uint32_t kk = (uint32_t)(j + D < 8 ? s * 8 + j + D : sn * 8 + j + D - 8) * 1024;
+#pragma unroll
+            for (int t = 0; t < NT; t++) bq[t][j % D] = bload16(rq, vq, q0[t] + kk);
+        }
+        // min term (src/ops/quant.rs:876-883): accm = sum_j m_j * bsum_j
+        v16f cm[NT];
+        float ds[NT];
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            cm[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, __builtin_bit_cast(v8h, bm[t]), v16f{}, 0, 0, 0);
+            ds[t] = dx[t];
+            bm[t] = bload16(rm, vq, m0[t] + (uint32_t)sn * 1024);
+            dx[t] = __builtin_bit_cast(float,
+                                       __builtin_amdgcn_raw_buffer_load_b32(rd, vd, d0[t] + (uint32_t)sn * 128, 0));
+        }
+        // epilogue (src/ops/quant.rs:849-898): element i of a lane is row 8*(i/4) + 4*g + i%4, token r
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 dv = *reinterpret_cast<const float4*>(dd + 8 * q + 4 * g);
+            const float4 mv = *reinterpret_cast<const float4*>(dd + 32 + 8 * q + 4 * g);
+            const float dr[4] = {dv.x, dv.y, dv.z, dv.w}, mr[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int i = 4 * q + e;
+#pragma unroll
+                for (int t = 0; t < NT; t++)
+                    p[t][i] = ((dr[e] * ds[t]) * (float)(8 * c1[t][i] + c0[t][i])) - ((mr[e] * ds[t]) * cm[t][i]);
+            }
+        }
+    };
+    auto lds_store = [&](int l, const float (&v)[NT][16]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                lv[((l - 2) * NT + t) * 256 + q * 64 + lane] =
+                    make_float4(v[t][4 * q], v[t][4 * q + 1], v[t][4 * q + 2], v[t][4 * q + 3]);
+    };
+    // v = (level l) + v: the stored block is the left operand
+    auto lds_merge = [&](int l, float (&v)[NT][16]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 u = lv[((l - 2) * NT + t) * 256 + q * 64 + lane];
+                v[t][4 * q] = u.x + v[t][4 * q];
+                v[t][4 * q + 1] = u.y + v[t][4 * q + 1];
+                v[t][4 * q + 2] = u.z + v[t][4 * q + 2];
+                v[t][4 * q + 3] = u.w + v[t][4 * q + 3];
+            }
+    };
+    auto reg_merge = [&](const float (&l)[NT][16], float (&v)[NT][16]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[t][i] = l[t][i] + v[t][i];
+    };
+    auto reg_copy = [&](float (&l)[NT][16], const float (&v)[NT][16]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) l[t][i] = v[t][i];
+    };
+
+    // fixed_tree (src/ops/quant.rs:461-476) as a binary counter over s: after
+    // leaf s the levels below L = (trailing ones of s) merge into level L.
+    int s = 0;
+    for (; s + 1 < R; s++) {
+        float p[NT][16];
+        sblock(s, p);
+        const int L = __builtin_ctz(~s);
+        if (L == 0) {
+            reg_copy(L0, p);
+        } else {
+            reg_merge(L0, p);
+            if (L == 1) {
+                reg_copy(L1, p);
+            } else {
+                reg_merge(L1, p);
+                if (L == 2) {
+                    lds_store(2, p);
+                } else {  // L == 3 (s = 7: R <= 16 leaves no higher level open before the last leaf)
+                    lds_merge(2, p);
+                    lds_store(3, p);
+                }
+            }
+        }
+    }
+    float res[NT][16];
+    {
+        // last leaf: merge the levels below L, then fold the blocks still open
+        // (the set bits of R above L) right to left
+        sblock(s, res);
+        const int L = __builtin_ctz(~s);
+        if (L >= 1) reg_merge(L0, res);
+        if (L >= 2) reg_merge(L1, res);
+        if (L >= 3) lds_merge(2, res);
+        if (L >= 4) lds_merge(3, res);
+        if (L < 1 && ((R >> 1) & 1)) reg_merge(L1, res);
+        if (L < 2 && ((R >> 2) & 1)) lds_merge(2, res);
+        if (L < 3 && ((R >> 3) & 1)) lds_merge(3, res);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int T = NT * tp + t, tok = T * 32 + r;
+        if (T < Mt && tok < M) {
+            float* yrow = y + (size_t)tok * N;
+            const bool vec = (N & 3) == 0;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int o = o0 + 8 * q + 4 * g;
+                if (vec && o + 3 < N) {
+                    *reinterpret_cast<float4*>(yrow + o) =
+                        make_float4(res[t][4 * q], res[t][4 * q + 1], res[t][4 * q + 2], res[t][4 * q + 3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (o + e < N) yrow[o + e] = res[t][4 * q + e];
+                }
+            }
+        }
+    }
+}
+
 size_t q4k_gemm_workspace_bytes(int batch, int in_feat) {
     const int Mp = (min(batch, kChunkM) + 31) / 32 * 32;
     const size_t R = in_feat / 256;
-    return align256((size_t)Mp * R * 256) + align256((size_t)Mp * R * 4) + (size_t)Mp * R * 16;
+    return align256((size_t)Mp * R * 256) + align256((size_t)Mp * R * 4) + (size_t)Mp * R * 32;
 }
 
 int q4k_gemm_max_in_feat() { return 127 * 256; }
@@ -312,6 +603,15 @@ template <int LV>
 static void launch_gemm_lv(dim3 grid, hipStream_t stream, const uint8_t* w, GemmWs ws, float* y, int R, int N, int M,
                            int NR, int TT) {
     hipLaunchKernelGGL(q4k_gemm_kernel<LV>, grid, dim3(256), 0, stream, w, ws, y, R, N, M, NR, TT);
+}
+
+static hipError_t launch_pw(hipStream_t stream, const uint8_t* w, GemmWs ws, float* y, int R, int N, int M, int Mt) {
+    const int NG = (N + 32 * kPwWaves - 1) / (32 * kPwWaves), TP = (Mt + 1) / 2;
+    const size_t lds = (size_t)kPwWaves * kPwLdsPerWave;
+    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(&q4k_gemm_pw_kernel), lds)) return e;
+    hipLaunchKernelGGL(q4k_gemm_pw_kernel, dim3((unsigned)NG * (unsigned)TP), dim3(kPwWaves * 64), lds, stream, w, ws,
+                       y, R, N, M, NG, TP);
+    return hipGetLastError();
 }
 
 hipError_t launch_q4k_gemm(const float* x, const uint8_t* w, float* y, int batch, int in_feat, int out_feat,
@@ -324,13 +624,20 @@ hipError_t launch_q4k_gemm(const float* x, const uint8_t* w, float* y, int batch
     for (int b0 = 0; b0 < batch; b0 += kChunkM) {
         const int M = min(batch - b0, kChunkM), Mp = (M + 31) / 32 * 32;
         const GemmWs ws = gemm_ws(workspace, Mp, R);
-        // Mp is a multiple of 32, so Mp / 16 groups cover every token slot
+        // rows of at most 16 super-blocks take the per-wave kernel (its buffer
+        // descriptors address the weights with 32-bit offsets); Mp is a
+        // multiple of 32, so Mp / 16 pre-pass groups cover every token slot
+        const bool pw = R <= kPwMaxR && (size_t)out_feat * R * 144 < ((size_t)1 << 31);
         hipLaunchKernelGGL(act_quant_tiles_kernel, dim3((unsigned)R, (unsigned)(Mp / kQuantWaves)),
-                           dim3(kQuantWaves * 64), 0, stream, x + (size_t)b0 * in_feat, ws, R, M);
+                           dim3(kQuantWaves * 64), 0, stream, x + (size_t)b0 * in_feat, ws, R, M, pw ? 1 : 0);
         if (hipError_t e = hipGetLastError()) return e;
+        float* yb = y + (size_t)b0 * out_feat;
+        if (pw) {
+            if (hipError_t e = launch_pw(stream, w, ws, yb, R, out_feat, M, Mp / 32)) return e;
+            continue;
+        }
         const int TT = (M + kTB - 1) / kTB;
         const dim3 grid((unsigned)NR * (unsigned)TT);
-        float* yb = y + (size_t)b0 * out_feat;
         switch (lv) {
         case 1: launch_gemm_lv<1>(grid, stream, w, ws, yb, R, out_feat, M, NR, TT); break;
         case 2: launch_gemm_lv<2>(grid, stream, w, ws, yb, R, out_feat, M, NR, TT); break;
