@@ -84,7 +84,10 @@ void vtq_destroy(vtq_ctx *ctx);
 /* Text of the last error on this context ("" after success); for
  * VTQ_E_INTERNAL it is the reference's Error::Internal message. */
 const char *vtq_last_error(const vtq_ctx *ctx);
-/* Library version string. */
+/* Library version string, "vtq <major>.<minor>.<patch> (gfx950)".  It names
+ * the ABI of this header and of vtq_runtime.h together; 0.2.0 added the
+ * trailing digest_v1 argument of vtqrt_run (a caller built against 0.1.0
+ * headers must not load this library). */
 const char *vtq_version(void);
 
 /* ---- host-pointer entry points (synchronous; y is complete on return) ----
@@ -141,7 +144,7 @@ int vtq_linear_device(vtq_ctx *ctx, int ggml_type, int regime, const float *d_x,
  * prefill GEMM's workspace (the quantized activations, batch >= 32 on Q4_K
  * in the integer regime) lives in a fixed 32 MiB array on each GPU,
  * allocated when the library loads.  Requests whose workspace would exceed
- * it (vtq::q4k_gemm_workspace_bytes: about batch x in_feat x 1.08 bytes,
+ * it (vtq::q4k_gemm_workspace_bytes: about batch x in_feat x 1.14 bytes,
  * batch capped at 8192 per chunk) return VTQ_E_NOT_IMPLEMENTED with a
  * message and launch nothing.  All calls on one GPU share that array:
  * calls that overlap in time on one device (any context, any stream) race

@@ -93,7 +93,8 @@ int vtqrt_transcendentals_device(const float *d_x, size_t n, float *d_y, void *s
  * seq_len; then what step 0 would report (embedding_row's texts, a norm
  * weight of the wrong length as VTQ_E_SHAPE_MISMATCH, each linear's
  * linear_dispatch error); then a prompt or generated token past the
- * embedding table.  Nothing is launched until these checks pass. */
+ * embedding table.  Nothing is launched until these checks pass.
+ * digest_v1 arrived in ABI 0.2.0 (vtq_version); NULL skips it. */
 int vtqrt_run(vtqrt_model *m, int regime, const char *model_id, const uint8_t weights_hash[32],
               const uint32_t *prompt, int prompt_len, int n_new, float *logits, uint32_t *tokens,
               uint8_t digest[32], uint8_t digest_v1[32]);

@@ -22,7 +22,8 @@ def declared_functions():
 def test_library_built_and_loads():
     assert os.path.exists(vtq.LIB_PATH), "run __graft_entry__.build()"
     lib = vtq.load_library()
-    assert lib.vtq_version().decode().startswith("vtq ")
+    # 0.2.0: vtqrt_run takes the trailing digest_v1 argument (include/vtq.h)
+    assert lib.vtq_version().decode().startswith("vtq 0.2.")
 
 
 def test_every_declared_symbol_is_exported():
