@@ -14,10 +14,16 @@
  * Pins: the libm and BLAKE3 restatements and the v2 digest are pinned by the
  * reference's own constants (tests/test_oracle_e2e.py); rms_norm, softmax
  * and argmax by the reference's known answers (src/ops/rms_norm.rs:117-160,
- * src/ops/argmax.rs:74-125) and closed forms.  Parity unpinned: the
- * composition of the forward step and run_quantized's token loop -- the
- * reference's model tests need GGUF files that are not in the repository,
- * and no reference-produced logits exist for any model here.
+ * src/ops/argmax.rs:74-125) and closed forms.  The composition of the
+ * forward step and run_quantized's token loop has no reference vector (the
+ * reference's model tests need GGUF files that are not in the repository);
+ * it is pinned through models on which the step reduces exactly to the
+ * parts above (tests/decode_compose.py, tests/test_decode_composition.py):
+ * zero output projections (the token loop and the head), the first step
+ * (residual wiring, SwiGLU, the GQA head map on v) and zero query weights
+ * (uniform softmax weights, the KV-cache indexing at every position).
+ * Parity unpinned: RoPE's placement and the attention scores with nonzero
+ * q, which none of those models exercises.
  */
 #include "vtq_oracle_e2e.h"
 #include "vtq_oracle.h"
