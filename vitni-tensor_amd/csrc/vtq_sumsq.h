@@ -290,7 +290,11 @@ __device__ inline float sumsq_walk(float s, const float* prod, int n, int H, con
         const int kr = k - 32 * (int)seg;
         const uint64_t b2 =
             __builtin_amdgcn_ballot_w64(lane < 32 && lane >= kr && (qt >= T || ((wt >> (lane & 31)) & 1u)));
-        const int el = (int)rdf((uint32_t)__builtin_ctzll(b2));  // b2 has a bit: the segment holds the event
+        if (b2 == 0) {  // the segment holds the event by construction; if not, the chain (s, k unchanged here)
+            fb = true;
+            break;
+        }
+        const int el = (int)rdf((uint32_t)__builtin_ctzll(b2));
         const int ev = 32 * (int)seg + el;
         const uint32_t qa = rdl(qt, max(el - 1, 0)), qb = rdl(v1, max((int)seg - 1, 0));
         const uint32_t qprev = el > 0 ? qa : (seg > 0 ? qb : 0u);  // prefix of terms before the event
