@@ -168,3 +168,71 @@ def zero_q_run(w, prompt, n_new):
         return w.head(x)
 
     return token_loop(prompt, n_new, logits_of)
+
+
+# ------------------------------------------------------- adversarial rows
+
+def _q4k_block(d_bits, dmin_bits, sc, m, qs):
+    """One Q4_K block from f16 d / dmin bits, 8 six-bit scales and mins and
+    256 four-bit codes (the packing get_scale_min_k4 reads,
+    src/ops/quant.rs:267-276)."""
+    s = np.zeros(12, np.uint8)
+    for j in range(4):
+        s[j] = (sc[j] & 63) | ((sc[j + 4] >> 4) << 6)
+        s[j + 4] = (m[j] & 63) | ((m[j + 4] >> 4) << 6)
+        s[j + 8] = (sc[j + 4] & 15) | ((m[j + 4] & 15) << 4)
+    q = np.asarray(qs, np.uint8).reshape(4, 2, 32)  # element 64h + 32hi + l
+    packed = (q[:, 0, :] | (q[:, 1, :] << 4)).reshape(128)
+    return np.concatenate([np.frombuffer(np.uint16(d_bits).tobytes(), np.uint8),
+                           np.frombuffer(np.uint16(dmin_bits).tobytes(), np.uint8), s, packed]).astype(np.uint8)
+
+
+def adversarial_row(kind, dim, rng):
+    """Q4_K bytes of one embedding row of the given kind: 'halves' (x = q/2,
+    squares with ties), 'short' (a 2^-6 grid), 'huge' (|x| up to 6.2e7),
+    'outliers' (one block 10^4 times the rest), 'nan', 'inf', 'zero'."""
+    nb = dim // 256
+    blocks = []
+    for b in range(nb):
+        qs = rng.integers(0, 16, 256)
+        sc, m, d, dmin = [1] * 8, [0] * 8, 0x3800, 0  # d = 0.5
+        if kind == "short":
+            sc, d = list(rng.integers(1, 4, 8)), 0x2400  # d = 2^-6
+        elif kind == "huge":
+            sc, d = [63] * 8, 0x7BFF  # d = 65504
+        elif kind == "outliers":
+            sc, m, d, dmin = list(rng.integers(1, 64, 8)), list(rng.integers(0, 64, 8)), 0x1E66, 0x1A66
+            if b == nb // 2:
+                d = 0x5A00  # 192: four orders of magnitude above the rest
+        elif kind == "nan" and b == nb - 1:
+            d = 0x7E00
+        elif kind == "inf" and b == 0:
+            d, qs = 0x7C00, np.maximum(qs, 1)
+        elif kind == "zero":
+            d, qs = 0, np.zeros(256, np.int64)
+        blocks.append(_q4k_block(d, dmin, sc, m, qs))
+    return np.concatenate(blocks)
+
+
+ADVERSARIAL_KINDS = ["halves", "short", "huge", "outliers", "nan", "inf", "zero"]
+
+
+def with_embedding_rows(blob, dim, rows):
+    """The blob with token_embd rows replaced: rows = {token: Q4_K bytes}."""
+    b = bytearray(bytes(blob))
+    _, t, off, size = G.tensor_table(b)["token_embd.weight"]
+    assert t == Q4_K
+    rb = dim // 256 * 144
+    for tok, data in rows.items():
+        assert data.size == rb and (tok + 1) * rb <= size
+        b[off + tok * rb:off + (tok + 1) * rb] = data.tobytes()
+    return bytes(b)
+
+
+def bits_equal_nan(got, want):
+    """Finite outputs bit for bit, the same NaN positions (IEEE leaves NaN
+    payloads unspecified), infinities exactly."""
+    got, want = np.asarray(got, F).reshape(-1), np.asarray(want, F).reshape(-1)
+    nan_g, nan_w = np.isnan(got), np.isnan(want)
+    return bool(np.array_equal(nan_g, nan_w) and
+                np.array_equal(got[~nan_w].view(np.uint32), want[~nan_w].view(np.uint32)))

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 import decode_compose as C
+import gguf_edit as G
 import oracle as O
 from vtq import synth
 
@@ -70,3 +71,29 @@ def test_reductions_are_not_vacuous():
     wz = C.Weights(C.zero_out_model(blob, SMALL["layers"]), SMALL)
     toks, lz = C.zero_out_run(wz, prompt, 3)
     assert len(set(map(int, toks))) > 1 or not np.array_equal(bits(lz[-1]), bits(lz[-2]))
+
+
+NORM_DIMS = [dict(dim=d, hidden=768, layers=1, heads=d // 64, kv_heads=d // 256, vocab=300, ctx=8,
+                  rope_theta=10000.0, rms_eps=1e-5) for d in (1024, 2048, 2560, 4096)]
+
+
+def adversarial_model(cfg, zero_wo):
+    blob, _ = synth.e2e_inputs(cfg, 2)
+    rng = np.random.default_rng(cfg["dim"])
+    rows = {1 + i: C.adversarial_row(k, cfg["dim"], rng) for i, k in enumerate(C.ADVERSARIAL_KINDS)}
+    blob = C.with_embedding_rows(blob, cfg["dim"], rows)
+    if zero_wo:  # the FFN's norm then sees the embedding row itself
+        blob = G.zero_tensors(blob, [f"blk.{l}.attn_output.weight" for l in range(cfg["layers"])])
+    return blob
+
+
+@pytest.mark.parametrize("zero_wo", [False, True], ids=["full", "zero-wo"])
+@pytest.mark.parametrize("cfg", NORM_DIMS, ids=[f"dim{c['dim']}" for c in NORM_DIMS])
+def test_first_step_on_adversarial_rows(cfg, zero_wo):
+    # the first step's norms on rows of ties, short mantissas, huge values,
+    # outliers, NaN, Inf and zeros (embedding rows of crafted Q4_K blocks)
+    blob = adversarial_model(cfg, zero_wo)
+    w = C.Weights(blob, cfg)
+    for tok in range(1, 1 + len(C.ADVERSARIAL_KINDS)):
+        _, logits = run_oracle(blob, np.array([tok, 0], np.uint32), 1)
+        assert C.bits_equal_nan(logits[0], C.step0_logits(w, tok)), C.ADVERSARIAL_KINDS[tok - 1]

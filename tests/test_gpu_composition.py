@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 import decode_compose as C
-from test_decode_composition import GQA4, IDS, SMALL, VARIANTS, WH, bits
+from test_decode_composition import IDS, NORM_DIMS, VARIANTS, WH, adversarial_model, bits
 from vtq import runtime, synth
 
 pytestmark = pytest.mark.gpu
@@ -81,3 +81,23 @@ def test_gpu_config5_shape_first_step():
     _, logits = run_gpu(blob, prompt, 1)
     want = C.step0_logits(C.Weights(blob, cfg, THREADS), int(prompt[0]))
     assert np.array_equal(bits(logits[0]), bits(want))
+
+
+@pytest.mark.parametrize("zero_wo", [False, True], ids=["full", "zero-wo"])
+@pytest.mark.parametrize("cfg", NORM_DIMS, ids=[f"dim{c['dim']}" for c in NORM_DIMS])
+def test_gpu_first_step_on_adversarial_rows(cfg, zero_wo):
+    # the fused normalising GEMVs on rows of ties, short mantissas, huge
+    # values, outliers, NaN, Inf and zeros: the QKV GEMV's norm prologue sees
+    # the embedding row, and with attn_output zero so does the W1/W3 SwiGLU
+    # kernel's; dims 1024-4096 take the binade walk, 2560 its longer head
+    blob = adversarial_model(cfg, zero_wo)
+    w = C.Weights(blob, cfg, THREADS)
+    m = runtime.Model(blob)
+    try:
+        for tok in range(1, 1 + len(C.ADVERSARIAL_KINDS)):
+            kind = C.ADVERSARIAL_KINDS[tok - 1]
+            print(f"[gpu] adversarial norm row {kind} dim {cfg['dim']} zero_wo={zero_wo}", flush=True)
+            _, _, logits = m.run(np.array([tok, 0], np.uint32), 1, WH)
+            assert C.bits_equal_nan(logits[0], C.step0_logits(w, tok)), kind
+    finally:
+        m.close()
