@@ -21,8 +21,8 @@
  *   VTQ_E_INTERNAL         Error::Internal(&'static str)  (shape/length;
  *                          vtq_last_error() returns the reference's text)
  *   VTQ_E_GPU              Error::GpuError                (HIP failure)
- *   VTQ_E_NOT_IMPLEMENTED  Error::NotImplemented          (F16/other dtypes,
- *                          in_feat beyond the kernels' limit)
+ *   VTQ_E_NOT_IMPLEMENTED  Error::NotImplemented          (F16/other dtypes; a
+ *                          request beyond the no-alloc entry point's scratch)
  *   VTQ_E_INVALID_ARGUMENT null pointer or context; Rust's types rule these out
  *   VTQ_E_MALFORMED        Error::Malformed               (GGUF parse, libvtq_runtime)
  *   VTQ_E_TRUNCATED        Error::Truncated               (GGUF parse, libvtq_runtime)
@@ -146,7 +146,12 @@ int vtq_linear_device(vtq_ctx *ctx, int ggml_type, int regime, const float *d_x,
  * allocated when the library loads.  Requests whose workspace would exceed
  * it (vtq::q4k_gemm_workspace_bytes: about batch x in_feat x 1.14 bytes,
  * batch capped at 8192 per chunk) return VTQ_E_NOT_IMPLEMENTED with a
- * message and launch nothing.  All calls on one GPU share that array:
+ * message and launch nothing.  Rows longer than the kernels hold (k-quant
+ * beyond 32768 inputs, the canonical dot beyond 65536) keep their
+ * segments' sums there too (segments x batch x out_feat x 4 bytes, plus one
+ * gathered segment of x per batch row for the canonical dot), with the
+ * batch split into passes that fit; a single batch row that does not fit
+ * is refused the same way.  All calls on one GPU share that array:
  * calls that overlap in time on one device (any context, any stream) race
  * on it and must be serialised by the caller.  Every byte a call reads from
  * the array is written earlier in the same call, so nothing needs clearing

@@ -335,14 +335,33 @@ def test_errors_mirror_reference(ctx):
         ctx.linear_q4_0(np.zeros(31, F), np.zeros(18, np.uint8), np.zeros(1, F), 1, 32, 1)
     with pytest.raises(vtq.Internal, match="x shorter"):
         ctx.linear_q4_k_integer(np.zeros(255, F), np.zeros(144, np.uint8), y, 1, 256, 1)
-    with pytest.raises(vtq.NotImplementedDtype, match="above 32768"):
-        ctx.linear(vtq.Q4_K, 0, np.zeros(32768 + 256, F), np.zeros((32768 + 256) // 256 * 144, np.uint8),
-                   np.zeros(1, F), 1, 32768 + 256, 1)
-    with pytest.raises(vtq.NotImplementedDtype, match="above 65536"):
-        ctx.linear(vtq.Q8_0, 0, np.zeros(65536 + 32, F), np.zeros((65536 + 32) // 32 * 34, np.uint8),
-                   np.zeros(1, F), 1, 65536 + 32, 1)
     # the context stays usable after errors
     test_q4k_integer_synthetic(ctx, 1, 256, 3)
+
+
+# Rows longer than the kernels hold (k-quant: 32768 inputs, the canonical dot:
+# 65536) run as aligned segments whose sums fixed_tree combines: one to five
+# segments, a last segment of one block or one chunk, batch rows gathered or
+# strided, and the GEMM batch size (>= 32) on rows too long for the GEMM.
+LONG_KQ = [(1, 49152, 5), (2, 32768 + 256, 7), (3, 65536 + 2048, 4), (1, 131072 + 4096, 3), (40, 40960, 3)]
+LONG_CANON = [(vtq.Q8_0, 0, 1, 65536 + 32, 3), (vtq.Q8_0, 0, 2, 2 * 65536 + 8192 + 32, 5),
+              (vtq.Q5_0, 0, 1, 73728, 3), (vtq.Q4_0, 0, 2, 73728, 2), (vtq.F32, 0, 1, 65536 + 7, 3),
+              (vtq.F32, 0, 2, 131073, 2), (vtq.Q4_K, 1, 1, 65536 + 256, 3), (vtq.Q4_K, 1, 2, 98304, 2)]
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", LONG_KQ)
+@pytest.mark.parametrize("ggml_type", [vtq.Q4_K, vtq.Q6_K])
+def test_kquant_long_rows_segmented(ctx, ggml_type, batch, in_f, out_f):
+    w = synth.weights(ggml_type, out_f, in_f, seed=in_f + 5 * out_f + ggml_type)
+    x = synth.activations(batch * in_f, seed=in_f * 3 + batch)
+    check(ctx, ggml_type, 0, x, w, batch, in_f, out_f)
+
+
+@pytest.mark.parametrize("ggml_type,regime,batch,in_f,out_f", LONG_CANON)
+def test_canonical_long_rows_segmented(ctx, ggml_type, regime, batch, in_f, out_f):
+    w = synth.weights(ggml_type, out_f, in_f, seed=in_f + 7 * out_f + ggml_type)
+    x = synth.activations(batch * in_f, seed=in_f * 5 + batch)
+    check(ctx, ggml_type, regime, x, w, batch, in_f, out_f)
 
 
 def test_weight_cache_rekeys_on_length_and_release(ctx):

@@ -55,6 +55,9 @@ def test_noalloc_matches_allocating_entry_point():
         # GEMV paths (no scratch), after the scratch holds stale data
         _run_both(ctx, vtq.Q4_K, 1, 11008, 4096, seed=17)
         _run_both(ctx, vtq.Q6_K, 1, 4096, 777, seed=19)
+        # rows longer than one segment: the segments' sums go through the scratch
+        _run_both(ctx, vtq.Q4_K, 3, 49152, 300, seed=23)
+        _run_both(ctx, vtq.Q6_K, 1, 32768 + 256, 100, seed=29)
     finally:
         ctx.close()
 

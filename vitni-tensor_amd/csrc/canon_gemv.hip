@@ -619,12 +619,13 @@ static hipError_t launch_q8_lds(const float* x, const uint8_t* w, size_t row_byt
     return hipErrorInvalidValue;
 }
 
+// wbytes: bytes readable from w (a segment launch starts inside the rows)
 template <class Dec>
 static hipError_t launch_pc(const float* x, const uint8_t* w, size_t row_bytes, float* y, int batch, int n,
-                            int out_feat, hipStream_t stream) {
+                            int out_feat, hipStream_t stream, size_t wbytes = 0) {
     const int nchunks = (n + kChunk - 1) / kChunk;
     const int nwin = (min(n, kChunk) + 255) / 256;
-    const size_t wbytes = row_bytes * (size_t)out_feat;
+    if (wbytes == 0) wbytes = row_bytes * (size_t)out_feat;
     int cpw = 1;
     while (cpw < nchunks) cpw <<= 1;
     const int rows = 8 / cpw;
@@ -689,6 +690,24 @@ hipError_t launch_canon_gemv(CanonFormat fmt, const float* x, const uint8_t* w, 
 
 int canon_max_in_feat() { return kMaxChunkSlots * kChunk; }
 
+hipError_t launch_canon_segment(CanonFormat fmt, const float* x, const uint8_t* w, size_t row_bytes, size_t w_avail,
+                                float* y, int batch, int seg_in, int out_feat, hipStream_t stream) {
+    if (seg_in <= 0 || seg_in > canon_max_in_feat()) return hipErrorInvalidValue;
+    if (seg_in % 4 == 0) {
+        switch (fmt) {
+        case kCanonQ8_0: return launch_pc<DecQ8_0>(x, w, row_bytes, y, batch, seg_in, out_feat, stream, w_avail);
+        case kCanonQ5_0: return launch_pc<DecQ5_0>(x, w, row_bytes, y, batch, seg_in, out_feat, stream, w_avail);
+        case kCanonQ4_0: return launch_pc<DecQ4_0>(x, w, row_bytes, y, batch, seg_in, out_feat, stream, w_avail);
+        case kCanonF32: return launch_pc<DecF32>(x, w, row_bytes, y, batch, seg_in, out_feat, stream, w_avail);
+        case kCanonQ4KFloat:
+            return launch_pc<DecQ4KFloat>(x, w, row_bytes, y, batch, seg_in, out_feat, stream, w_avail);
+        }
+        return hipErrorInvalidValue;
+    }
+    // the per-lane form reads only inside each row's segment
+    return launch_canon_gemv(fmt, x, w, row_bytes, y, batch, seg_in, out_feat, 0, stream);
+}
+
 __global__ void fill_kernel(float* __restrict__ y, size_t n, float v) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) y[i] = v;
@@ -697,6 +716,61 @@ __global__ void fill_kernel(float* __restrict__ y, size_t n, float v) {
 hipError_t launch_fill(float* y, size_t n, float v, hipStream_t stream) {
     if (n == 0) return hipSuccess;
     hipLaunchKernelGGL(fill_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, y, n, v);
+    return hipGetLastError();
+}
+
+__global__ void gather_cols_kernel(const float* __restrict__ x, size_t ld, size_t col0, int ncol,
+                                   float* __restrict__ out) {
+    const size_t b = blockIdx.y;
+    for (int c = (int)(blockIdx.x * blockDim.x + threadIdx.x); c < ncol; c += (int)(gridDim.x * blockDim.x))
+        out[b * (size_t)ncol + c] = x[b * ld + col0 + c];
+}
+
+hipError_t launch_gather_cols(const float* x, size_t ld, size_t col0, int ncol, int batch, float* out,
+                              hipStream_t stream) {
+    if (ncol <= 0 || batch <= 0) return hipSuccess;
+    const unsigned gx = (unsigned)min((ncol + 255) / 256, 1024);
+    hipLaunchKernelGGL(gather_cols_kernel, dim3(gx, (unsigned)batch), dim3(256), 0, stream, x, ld, col0, ncol, out);
+    return hipGetLastError();
+}
+
+// fixed_tree (src/ops/quant.rs:461-476) over the segments of each output,
+// streamed as a binary counter: after leaf s the levels below L = (trailing
+// ones of s) merge into level L, the stored block being the left operand;
+// at the end the open blocks (the set bits of nseg) fold right to left.
+constexpr int kTreeLevels = 17;  // nseg < 2^17
+__global__ void segment_tree_kernel(const float* __restrict__ part, size_t n, int nseg, float* __restrict__ y) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float stk[kTreeLevels];
+#pragma unroll
+    for (int l = 0; l < kTreeLevels; l++) stk[l] = 0.0f;
+    for (int s = 0; s < nseg; s++) {
+        float p = part[(size_t)s * n + i];
+        const int L = __builtin_ctz(~(unsigned)s);
+#pragma unroll
+        for (int l = 0; l < kTreeLevels; l++)
+            if (l < L) p = stk[l] + p;
+#pragma unroll
+        for (int l = 0; l < kTreeLevels; l++)
+            if (l == L) stk[l] = p;
+    }
+    float r = 0.0f;
+    bool have = false;
+#pragma unroll
+    for (int l = 0; l < kTreeLevels; l++) {
+        if ((nseg >> l) & 1) {
+            r = have ? stk[l] + r : stk[l];
+            have = true;
+        }
+    }
+    y[i] = r;
+}
+
+hipError_t launch_segment_tree(const float* part, size_t n, int nseg, float* y, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    if (nseg <= 0 || nseg >= (1 << kTreeLevels)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(segment_tree_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, part, n, nseg, y);
     return hipGetLastError();
 }
 

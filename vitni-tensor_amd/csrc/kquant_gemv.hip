@@ -423,9 +423,9 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
     constexpr int RPS = HALF ? 2 : 1;  // rows per wave step
     const int g = HALF ? ((lane >> 2) & 7) : (lane >> 2), k = lane & 3, hh = HALF ? lane >> 5 : 0;
     const int out_feat = EPI == kEpiSwiGLU ? args.rows[0] : args.rows[0] + args.rows[1] + args.rows[2];
-    const float* xb = x + (size_t)blockIdx.y * R * 256;
+    const float* xb = x + (size_t)blockIdx.y * (args.x_stride ? (size_t)args.x_stride : (size_t)R * 256);
     float* yb = y + (size_t)blockIdx.y * out_feat;
-    const uint32_t row_bytes = (uint32_t)R * Fmt::kBytes;
+    const uint32_t row_bytes = args.row_stride ? args.row_stride : (uint32_t)R * Fmt::kBytes;
     static_assert(PREW == 0 || (PRE == 0 && PREW < NWIN && !POSTX), "PREW splits row 0 of a PRE = 0 ring");
     const int tw = gridDim.x * kNW;
     const int gw = 4 * ((int)blockIdx.x + (int)gridDim.x * (wave >> 2)) + (wave & 3);
@@ -645,18 +645,22 @@ __global__ __launch_bounds__(kNW * 64) void kquant_rows_kernel(const float* __re
 // a branch would force the compiler to wait for all outstanding loads; with
 // straight-line loads each wait covers exactly the data it needs.  Results
 // are kept in registers and stored once at the end for the same reason.
+// row_stride (bytes between weight rows) and x_stride (floats between batch
+// rows of x) exceed R * block bytes and R * 256 when the launch is one
+// segment of longer rows.
 template <class Fmt, int D>
 __global__ __launch_bounds__(kNW * 64) void kquant_windows_kernel(const float* __restrict__ x,
                                                                   const uint8_t* __restrict__ W,
-                                                                  float* __restrict__ y, int R, int out_feat) {
+                                                                  float* __restrict__ y, int R, int out_feat,
+                                                                  size_t row_stride, size_t x_stride) {
     extern __shared__ __align__(16) unsigned char lds[];
     const ActLds act = act_lds_layout(lds, R);
     const int lane = threadIdx.x & 63;
     const int wave = wave_id();
     const int g = lane >> 2, k = lane & 3;
-    const float* xb = x + (size_t)blockIdx.y * R * 256;
+    const float* xb = x + (size_t)blockIdx.y * x_stride;
     float* yb = y + (size_t)blockIdx.y * out_feat;
-    const size_t row_bytes = (size_t)R * Fmt::kBytes;
+    const size_t row_bytes = row_stride;
     const int nwin = (R + 15) >> 4;
 
     // this wave's contiguous rows (at most 64: the launcher sizes the grid)
@@ -804,27 +808,33 @@ static hipError_t launch_rows(int nwin, int wgs, int batch, int R, const float* 
     }
 }
 
+// row_stride / x_stride: 0 for a whole matrix, else the strides of a segment
 template <class Fmt>
 static hipError_t launch_kq(const float* x, const uint8_t* w, float* y, int batch, int in_feat, int out_feat,
-                            int num_cus, hipStream_t stream) {
+                            int num_cus, hipStream_t stream, size_t row_stride = 0, int x_stride = 0) {
     const int R = in_feat / 256;
     const int nwin = (R + 15) / 16;
     const int wgs = rows_grid(out_feat, num_cus);
-    const size_t bytes = (size_t)out_feat * R * Fmt::kBytes;
+    const size_t rs = row_stride ? row_stride : (size_t)R * Fmt::kBytes;
+    const size_t xs = x_stride ? (size_t)x_stride : (size_t)R * 256;
+    const size_t bytes = (size_t)out_feat * rs;
     if (nwin <= Fmt::kRowsMaxWindows && bytes < (size_t)kOutOfRange) {
-        const RowsArgs a{{w, w, w}, {out_feat, 0, 0}, nullptr, 0.0f};
+        RowsArgs a{{w, w, w}, {out_feat, 0, 0}, nullptr, 0.0f};
+        a.row_stride = (uint32_t)rs;
+        a.x_stride = (int)xs;
         return launch_rows<Fmt, kEpiStore, false>(nwin, wgs, batch, R, x, a, y, stream);
     }
     const long waves = (long)wgs * kNW;
     const long units = ((long)out_feat + waves - 1) / waves * nwin;  // per wave, upper bound
     // 16 waves per CU leave 128 VGPRs per wave: at most 4 (Q4_K) / 2 (Q6_K) units in flight
     constexpr int kMaxD = sizeof(typename Fmt::Regs) > 48 ? 2 : 4;
-    if (units <= 1) return launch(kquant_windows_kernel<Fmt, 1>, wgs, batch, R, stream, x, w, y, R, out_feat);
+    if (units <= 1) return launch(kquant_windows_kernel<Fmt, 1>, wgs, batch, R, stream, x, w, y, R, out_feat, rs, xs);
     if constexpr (kMaxD == 2) {
-        return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, stream, x, w, y, R, out_feat);
+        return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, stream, x, w, y, R, out_feat, rs, xs);
     } else {
-        if (units <= 2) return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, stream, x, w, y, R, out_feat);
-        return launch(kquant_windows_kernel<Fmt, 4>, wgs, batch, R, stream, x, w, y, R, out_feat);
+        if (units <= 2)
+            return launch(kquant_windows_kernel<Fmt, 2>, wgs, batch, R, stream, x, w, y, R, out_feat, rs, xs);
+        return launch(kquant_windows_kernel<Fmt, 4>, wgs, batch, R, stream, x, w, y, R, out_feat, rs, xs);
     }
 }
 
@@ -883,6 +893,16 @@ hipError_t launch_q4k_gemv(const float* x, const uint8_t* w, float* y, int batch
 hipError_t launch_q6k_gemv(const float* x, const uint8_t* w, float* y, int batch, int in_feat, int out_feat,
                            int num_cus, hipStream_t stream) {
     return launch_kq<Q6K>(x, w, y, batch, in_feat, out_feat, num_cus, stream);
+}
+
+hipError_t launch_kquant_segment(int ggml_type, const float* x, int x_stride, const uint8_t* w, size_t row_stride,
+                                 float* y, int batch, int seg_in, int out_feat, int num_cus, hipStream_t stream) {
+    if (seg_in <= 0 || seg_in % 256 || seg_in > kquant_max_in_feat()) return hipErrorInvalidValue;
+    if (ggml_type == 12)
+        return launch_kq<Q4K>(x, w, y, batch, seg_in, out_feat, num_cus, stream, row_stride, x_stride);
+    if (ggml_type == 14)
+        return launch_kq<Q6K>(x, w, y, batch, seg_in, out_feat, num_cus, stream, row_stride, x_stride);
+    return hipErrorInvalidValue;
 }
 
 int kquant_max_in_feat() { return kMaxWindows * 16 * 256; }

@@ -116,8 +116,6 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
             p->row_bytes = (in_feat / 256) * kQ4K;
             if (!mul_ok(out_feat, p->row_bytes, &need) || w_len < need)
                 return set_err(c, VTQ_E_INTERNAL, "linear_q4_k_fused: weight shape mismatch");
-            if (in_feat > (size_t)vtq::canon_max_in_feat())
-                return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 65536 for the canonical dot");
             p->kind = Plan::kCanon;
             p->fmt = vtq::kCanonQ4KFloat;
         } else if (regime == VTQ_REGIME_INTEGER) {
@@ -128,8 +126,6 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
             if (!mul_ok(out_feat, p->row_bytes, &need) || w_len < need)
                 return set_err(c, VTQ_E_INTERNAL, serial_names ? "linear_q4_k_integer: weight shape mismatch"
                                                                : "linear_q4_k_integer_parallel: weight shape");
-            if (in_feat > (size_t)vtq::kquant_max_in_feat())
-                return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 32768 for k-quant GEMV");
             p->kind = (batch >= (size_t)vtq::kGemmMinBatch && in_feat <= (size_t)vtq::q4k_gemm_max_in_feat())
                           ? Plan::kQ4KGemm
                           : Plan::kQ4KInt;
@@ -145,8 +141,6 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
         if (!mul_ok(out_feat, p->row_bytes, &need) || w_len < need)
             return set_err(c, VTQ_E_INTERNAL, serial_names ? "linear_q6_k_integer: weight shape mismatch"
                                                            : "linear_q6_k_integer_parallel: weight shape");
-        if (in_feat > (size_t)vtq::kquant_max_in_feat())
-            return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 32768 for k-quant GEMV");
         p->kind = Plan::kQ6KInt;
         break;
     case VTQ_TYPE_Q8_0:
@@ -159,8 +153,6 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
         if (!mul_ok(out_feat, p->row_bytes, &need) || w_len < need)
             return set_err(c, VTQ_E_INTERNAL, q8 ? "linear_dispatch Q8_0: weight blob too small"
                                                  : "linear_dispatch Q5_0: weight blob too small");
-        if (in_feat > (size_t)vtq::canon_max_in_feat())
-            return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 65536 for the canonical dot");
         p->kind = Plan::kCanon;
         p->fmt = q8 ? vtq::kCanonQ8_0 : vtq::kCanonQ5_0;
         break;
@@ -170,16 +162,12 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
         p->row_bytes = (in_feat / 32) * kQ4_0;
         if (!mul_ok(out_feat, p->row_bytes, &need) || w_len != need)
             return set_err(c, VTQ_E_INTERNAL, "linear_q4_0: weight blob length mismatch");
-        if (in_feat > (size_t)vtq::canon_max_in_feat())
-            return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 65536 for the canonical dot");
         p->kind = Plan::kCanon;
         p->fmt = vtq::kCanonQ4_0;
         break;
     case VTQ_TYPE_F32:
         if (!mul_ok(in_feat, 4, &p->row_bytes) || !mul_ok(out_feat, p->row_bytes, &need) || w_len != need)
             return set_err(c, VTQ_E_INTERNAL, "linear_dispatch F32: weight size mismatch");
-        if (in_feat > (size_t)vtq::canon_max_in_feat())
-            return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: in_feat above 65536 for the canonical dot");
         p->kind = Plan::kCanon;
         p->fmt = vtq::kCanonF32;
         break;
@@ -191,17 +179,94 @@ int plan_linear(vtq_ctx* c, int type, int regime, size_t w_len, size_t batch, si
     return VTQ_OK;
 }
 
+// Rows longer than the kernels hold run as aligned segments (see
+// vtq_kernels.h): the segment length in inputs, or 0 when the plan needs none.
+size_t segment_inputs(const Plan& p, size_t in_feat) {
+    if ((p.kind == Plan::kQ4KInt || p.kind == Plan::kQ6KInt) && in_feat > (size_t)vtq::kquant_max_in_feat())
+        return (size_t)vtq::kquant_max_in_feat();
+    if (p.kind == Plan::kCanon && in_feat > (size_t)vtq::canon_max_in_feat()) return (size_t)vtq::canon_max_in_feat();
+    return 0;
+}
+
+// Batch rows per pass of a segmented plan and the workspace that pass needs:
+// the segments' y slices, plus (canonical dot, batch > 1) one segment of x
+// gathered into contiguous rows.  Passes are sized to stay under `cap`
+// bytes where one batch row fits; 0 rows if not even one does.
+size_t segment_rows(const Plan& p, size_t batch, size_t in_feat, size_t out_feat, size_t cap, size_t* ws_bytes) {
+    const size_t seg = segment_inputs(p, in_feat), nseg = (in_feat + seg - 1) / seg;
+    const bool gather = p.kind == Plan::kCanon;
+    auto need = [&](size_t rows) {
+        return (nseg * rows * out_feat + (gather && rows > 1 ? rows * seg : 0)) * 4 + 256;
+    };
+    size_t rows = batch < 65535 ? batch : 65535;
+    while (rows > 1 && need(rows) > cap) rows = (rows + 1) / 2;
+    *ws_bytes = need(rows);
+    return need(rows) <= cap ? rows : 0;
+}
+
+int run_segmented(vtq_ctx* c, const Plan& p, const float* dx, const uint8_t* dw, float* dy, size_t batch,
+                  size_t in_feat, size_t out_feat, hipStream_t s, void* fixed_ws, size_t fixed_ws_bytes) {
+    const size_t seg = segment_inputs(p, in_feat), nseg = (in_feat + seg - 1) / seg;
+    size_t ws_bytes = 0;
+    const size_t rows = segment_rows(p, batch, in_feat, out_feat, fixed_ws ? fixed_ws_bytes : ((size_t)256 << 20),
+                                     &ws_bytes);
+    if (rows == 0)
+        return set_err(c, VTQ_E_NOT_IMPLEMENTED, "vtq: the segment workspace of one batch row exceeds the scratch");
+    void* ws = fixed_ws;
+    if (!ws) {
+        if (int rc = grow_dev(c, c->ws, ws_bytes)) return rc;
+        ws = c->ws.ptr;
+    }
+    float* part = static_cast<float*>(ws);
+    hipError_t e = hipSuccess;
+    for (size_t b0 = 0; b0 < batch; b0 += rows) {
+        const int nb = (int)(batch - b0 < rows ? batch - b0 : rows);
+        float* xg = part + nseg * (size_t)nb * out_feat;
+        for (size_t k = 0; k < nseg; k++) {
+            const size_t i0 = k * seg;
+            const int len = (int)(in_feat - i0 < seg ? in_feat - i0 : seg);
+            float* yk = part + k * (size_t)nb * out_feat;
+            if (p.kind == Plan::kCanon) {
+                // byte offset of input i0 in a row: i0 is a multiple of every block size
+                const size_t off = p.fmt == vtq::kCanonF32 ? i0 * 4
+                                   : p.fmt == vtq::kCanonQ8_0 ? i0 / 32 * kQ8_0
+                                   : p.fmt == vtq::kCanonQ5_0 ? i0 / 32 * kQ5_0
+                                   : p.fmt == vtq::kCanonQ4_0 ? i0 / 32 * kQ4_0
+                                                               : i0 / 256 * kQ4K;
+                const float* xs = dx + b0 * in_feat + i0;
+                if (nb > 1) {
+                    e = vtq::launch_gather_cols(dx + b0 * in_feat, in_feat, i0, len, nb, xg, s);
+                    if (e != hipSuccess) return hip_fail(c, e, "kernel launch");
+                    xs = xg;
+                }
+                e = vtq::launch_canon_segment(p.fmt, xs, dw + off, p.row_bytes, p.w_need - off, yk, nb, len,
+                                              (int)out_feat, s);
+            } else {
+                const size_t off = i0 / 256 * (p.kind == Plan::kQ4KInt ? kQ4K : kQ6K);
+                e = vtq::launch_kquant_segment(p.kind == Plan::kQ4KInt ? 12 : 14, dx + b0 * in_feat + i0, (int)in_feat,
+                                               dw + off, p.row_bytes, yk, nb, len, (int)out_feat, c->num_cus, s);
+            }
+            if (e != hipSuccess) return hip_fail(c, e, "kernel launch");
+        }
+        e = vtq::launch_segment_tree(part, (size_t)nb * out_feat, (int)nseg, dy + b0 * out_feat, s);
+        if (e != hipSuccess) return hip_fail(c, e, "kernel launch");
+    }
+    return VTQ_OK;
+}
+
 // Enqueue the kernels of a validated plan.  `fixed_ws` (when not null) is a
-// caller-provided GEMM workspace already checked to be large enough; else the
-// context's workspace grows on demand.
+// caller-provided workspace of `fixed_ws_bytes` (the GEMM's size already
+// checked); else the context's workspace grows on demand.
 int run_plan(vtq_ctx* c, const Plan& p, const float* dx, const uint8_t* dw, float* dy, size_t batch,
-             size_t in_feat, size_t out_feat, hipStream_t s, void* fixed_ws = nullptr) {
+             size_t in_feat, size_t out_feat, hipStream_t s, void* fixed_ws = nullptr, size_t fixed_ws_bytes = 0) {
     if (batch == 0 || out_feat == 0) return VTQ_OK;
     hipError_t e = hipSuccess;
     if (in_feat == 0) {  // every reduction is over nothing: fixed_tree([]) == 0.0
         e = vtq::launch_fill(dy, batch * out_feat, 0.0f, s);
         return e == hipSuccess ? VTQ_OK : hip_fail(c, e, "fill");
     }
+    if (segment_inputs(p, in_feat)) return run_segmented(c, p, dx, dw, dy, batch, in_feat, out_feat, s, fixed_ws,
+                                                         fixed_ws_bytes);
     if (p.kind == Plan::kQ4KGemm) {
         // the launcher walks the batch in chunks that fit the workspace
         void* ws = fixed_ws;
@@ -474,7 +539,8 @@ int vtq_linear_device_noalloc(vtq_ctx* c, int type, int regime, const float* d_x
                        "vtq_linear_device_noalloc: the GEMM workspace of batch x in_feat exceeds the 32 MiB scratch");
     hipError_t e = hipSetDevice(c->device);
     if (e != hipSuccess) return hip_fail(c, e, "hipSetDevice");
-    return run_plan(c, p, d_x, d_w, d_y, batch, in_feat, out_feat, static_cast<hipStream_t>(stream), c->scratch_ptr);
+    return run_plan(c, p, d_x, d_w, d_y, batch, in_feat, out_feat, static_cast<hipStream_t>(stream), c->scratch_ptr,
+                    kScratchBytes);
 }
 
 }  // extern "C"
