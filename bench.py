@@ -155,6 +155,52 @@ def stream_ceiling(dw, timer, reps):
             "gb_s": round(nbytes / us / 1e3, 1), "frac_of_peak": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
+READ_WORKGROUPS = (1024, 2048, 4096, 8192)
+
+
+def read_ceiling(nbytes, timer, reps):
+    """A hand-written read-only stream (libvtq_probe's stream_read_kernel:
+    grid-stride 16-byte loads, one in flight per thread, no writes) over
+    `nbytes` rotated over > 600 MB of copies, graph-replayed like the GEMVs:
+    the read rate a plain access pattern reaches on buffers of this size,
+    launch floor included.  The best of a few grid sizes is kept."""
+    import torch
+
+    from vtq import probe
+
+    n = (nbytes + 15) // 16 * 16
+    copies = max(2, -(-ROTATE_MIN_BYTES // n))
+    bufs = [torch.ones(n, dtype=torch.uint8, device="cuda:0") for _ in range(copies)]
+    sink = torch.zeros(max(READ_WORKGROUPS), dtype=torch.int32, device="cuda:0")
+    per_wg = {}
+    for wg in READ_WORKGROUPS:
+        per_wg[wg] = statistics.median(timer.per_launch_us(
+            lambda k, cs, wg=wg: probe.stream_read(bufs[k % copies].data_ptr(), n, wg, sink.data_ptr(), cs),
+            LAUNCHES_PER_REPLAY, reps))
+    wg = min(per_wg, key=per_wg.get)
+    us = per_wg[wg]
+    del bufs, sink
+    torch.cuda.empty_cache()
+    return {"kernel": "stream_read_kernel (libvtq_probe): read-only grid-stride 16-byte loads of rotated copies, "
+                      "graph-replayed", "bytes_per_launch": n, "weight_copies_rotated": copies, "workgroups": wg,
+            "us_per_launch": round(us, 3), "us_per_launch_by_workgroups": {str(k): round(v, 3) for k, v in per_wg.items()},
+            "gb_s": round(n / us / 1e3, 1), "frac_of_peak": round(n / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def gemm_counters():
+    """The committed rocprofv3 SQ-counter summary of the prefill GEMM
+    (profiles/q4k_gemm_prefill_sq_counters.json): MFMA busy fraction of the
+    matrix cores over the kernel's duration, with the command that made it."""
+    path = os.path.join(ROOT, "profiles", "q4k_gemm_prefill_sq_counters.json")
+    if not os.path.exists(path):
+        return None
+    d = json.load(open(path))
+    return {"mfma_busy_frac": d["derived"]["mfma_busy_frac"],
+            "valu_mfma_coexec_frac_of_mfma_busy": d["derived"]["valu_mfma_coexec_frac_of_mfma_busy"],
+            "kernel": d["kernel"], "source": "profiles/q4k_gemm_prefill_sq_counters.json",
+            "command": d["command"]}
+
+
 def mfma_ceiling(m, k_, nn, timer, reps):
     """hipBLASLt's int8 GEMM (torch._int_mm) at the prefill shape: the int8
     rate a vendor GEMM reaches (a plain int32 product, not the reference's
@@ -254,13 +300,20 @@ def config_figures(ctx, cfg, timer, reps, cpu_seconds, with_cpu):
         out.update({"bound": "mfma", "tops": round(ops / us / 1e6, 1), "peak_tops": INT8_MFMA_PEAK_TOPS,
                     "frac": round(ops / us / 1e6 / INT8_MFMA_PEAK_TOPS, 4),
                     "tops_mall_warm": round(ops / us_warm / 1e6, 1),
-                    "kernel": "q4k_gemm_kernel (+ act_quant_tiles_kernel)"})
+                    "kernel": "q4k_gemm_pw_kernel (+ act_quant_tiles_kernel)"})
+        mc = gemm_counters()
+        if mc:
+            out["mfma_util_rocprof"] = mc
     else:
         nb = cfg.algorithmic_bytes()
         out.update({"bound": "hbm", "algorithmic_bytes": nb, "gb_s": round(nb / us / 1e3, 1),
                     "peak_gb_s": HBM_PEAK_GBS, "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
                     "gb_s_mall_warm": round(nb / us_warm / 1e3, 1),
                     "kernel": KERNEL_NAME.get(cfg.ggml_type, "?")})
+        rc = read_ceiling(nb, timer, reps)
+        out["read_ceiling"] = {"gb_s": rc["gb_s"], "us_per_launch": rc["us_per_launch"],
+                               "workgroups": rc["workgroups"]}
+        out["frac_of_measured_read"] = round(nb / us / 1e3 / rc["gb_s"], 4)
     if with_cpu:
         sec, n = cpu_time(lambda: oracle.linear_dispatch(cfg.ggml_type, 0, L.x, L.w, cfg.batch, cfg.in_feat,
                                                          cfg.out_feat, threads), cpu_seconds)
@@ -430,7 +483,7 @@ def main():
         },
         "roofline": {
             "bound": "mfma" if gemm else "hbm",
-            "kernel": f"{'q4k_gemm_kernel' if gemm else KERNEL_NAME.get(dc.ggml_type, '?')} "
+            "kernel": f"{'q4k_gemm_pw_kernel' if gemm else KERNEL_NAME.get(dc.ggml_type, '?')} "
                       f"{dc.out_feat}x{dc.in_feat} batch {dc.batch} (the step's slowest launch)",
             "achieved": round(achieved, 2),
             "peak": peak,
@@ -445,6 +498,10 @@ def main():
         },
     }
     ceilings = {"stream": stream_ceiling([L.dw for L in lins], timer, args.reps)}
+    if gemm:
+        mc = gemm_counters()
+        if mc:
+            out["roofline"]["mfma_util_rocprof"] = mc
     if not args.no_cpu:
         def cpu_step():
             for L in lins:
@@ -460,6 +517,15 @@ def main():
                       f"CPU share per GPU"}
     for L in lins:
         L.release()
+    if not gemm:
+        # the same bytes read by a plain read-only stream: the measured ceiling of this access size
+        rd = {}
+        for c in cfgs:
+            rd.setdefault(c.algorithmic_bytes(), read_ceiling(c.algorithmic_bytes(), timer, args.reps))
+        ceilings["read"] = list(rd.values())
+        rdom = rd[dc.algorithmic_bytes()]
+        out["roofline"]["measured_read_ceiling_gb_s"] = rdom["gb_s"]
+        out["roofline"]["frac_of_measured_read"] = round(achieved / rdom["gb_s"], 4)
     if args.workload == "q4k_gemv_ffn_pair" and not args.no_configs:
         # every BASELINE configuration in the same run
         figs = {}
