@@ -68,6 +68,17 @@ def test_e2e_wide_long_context():
     compare(WIDE, 250, 12, regimes=(0,), threads=16)
 
 
+# A context too long for the attention kernel's LDS (30000 scores beside the
+# cached-v tiles): every head keeps its scores in a row of HBM.  Positions
+# past 256 also take the tiled path of the weighted sum.
+LONG_CTX = dict(dim=256, hidden=512, layers=2, heads=4, kv_heads=2, vocab=1000, ctx=30000, rope_theta=10000.0,
+                rms_eps=1e-5)
+
+
+def test_e2e_context_beyond_lds_scores():
+    compare(LONG_CTX, 280, 10, regimes=(0,), threads=16)
+
+
 def test_e2e_walk_row_bounds():
     compare(WALK_LO, 5, 9, regimes=(0,))
     compare(WALK_HI, 5, 9, regimes=(0,), threads=16)

@@ -45,13 +45,18 @@ struct AttnArgs {
     int heads, kv_heads, head_dim, seq;
     float theta;
     int neox;                    // 1: RoPE on (j, j + head/2) pairs, 0: on (2j, 2j+1)
+    // the heads' score rows in HBM, [heads][seq rounded up to 4], where
+    // attention_scores_in_lds is false; nullptr otherwise
+    float* att_g = nullptr;
 };
 // RoPE of q and of this step's k, the cache write of k and v at *pos, and
 // per-head softmax attention (src/model/forward_quantized.rs:405-560).
 // attention_supported: whether the kernel takes this head dimension (a
-// multiple of 4 up to 256 that divides 16384) and cache length (its scores
-// fit in LDS beside the tiles).
+// multiple of 4 up to 256 that divides 16384); any cache length is taken.
+// attention_scores_in_lds: whether a head's seq scores fit in LDS beside the
+// cached-v tiles; else they go to the caller's att_g rows.
 bool attention_supported(int head_dim, int seq);
+bool attention_scores_in_lds(int head_dim, int seq);
 hipError_t attention(const AttnArgs& a, hipStream_t stream);
 
 // The embedding table, for the next step's row (see embed).

@@ -184,7 +184,8 @@ __device__ float block_max(float m, float* red) {
 }
 
 // One workgroup per query head h.  Shared: q (roped), this step's k (roped)
-// and v of h's KV head, then the attention weights of positions 0..pos.
+// and v of h's KV head, then the attention weights of positions 0..pos (in
+// LDS, or for contexts too long for it in the head's row of a.att_g).
 // HD > 0: the head dimension as a compile-time constant; with HD == 64 and
 // pos < kAttnThreads the position is read first, every load that does not
 // need it (q, k, v, the rope angles, thread t's cached k row) is issued
@@ -201,8 +202,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float* kp = qs + hd;
     float* vp = kp + hd;
     float* red = vp + hd;
-    float* att = red + kAttnThreads + (4 - (3 * hd) % 4) % 4;  // 16-byte aligned for float4 reads
-    float* vt = att + ((a.seq + 3) & ~3);
+    float* att_l = red + kAttnThreads + (4 - (3 * hd) % 4) % 4;  // 16-byte aligned for float4 reads
+    const size_t seq4 = ((size_t)a.seq + 3) & ~(size_t)3;
+    float* att = a.att_g ? a.att_g + (size_t)h * seq4 : att_l;
+    float* vt = a.att_g ? att_l : att_l + seq4;
     const int t0 = threadIdx.x;
     constexpr bool kFast = HD == 64;
     // The position first, then every load that does not need it: q, k, v
@@ -521,21 +524,36 @@ static hipError_t launch_attention(const AttnArgs& a, size_t lds, hipStream_t st
     return hipGetLastError();
 }
 
-static size_t attention_lds(int head_dim, int seq) {
-    return ((size_t)3 * head_dim + kAttnThreads + 4 + (((size_t)seq + 3) & ~(size_t)3) + kAttnTile * 64) * 4;
+// LDS bytes: q, k, v, the reduction slots, (the scores,) the v tiles
+static size_t attention_lds(int head_dim, int seq, bool scores) {
+    return ((size_t)3 * head_dim + kAttnThreads + 4 + (scores ? (((size_t)seq + 3) & ~(size_t)3) : 0) +
+            kAttnTile * 64) * 4;
 }
 
 bool attention_supported(int head_dim, int seq) {
     return head_dim > 0 && head_dim <= kAttnThreads && head_dim % 4 == 0 && (kAttnTile * 64) % head_dim == 0 &&
-           seq > 0 && attention_lds(head_dim, seq) <= 160 * 1024;
+           seq > 0;
+}
+
+bool attention_scores_in_lds(int head_dim, int seq) {
+    return attention_lds(head_dim, seq, true) <= 160 * 1024;
 }
 
 hipError_t attention(const AttnArgs& a, hipStream_t stream) {
     if (!attention_supported(a.head_dim, a.seq)) return hipErrorInvalidValue;
-    const size_t lds = attention_lds(a.head_dim, a.seq);
-    if (a.head_dim == 64) return launch_attention<64>(a, lds, stream);
-    if (a.head_dim == 128) return launch_attention<128>(a, lds, stream);
-    return launch_attention<0>(a, lds, stream);
+    const bool in_lds = attention_scores_in_lds(a.head_dim, a.seq);
+    if (!in_lds && !a.att_g) return hipErrorInvalidValue;
+    const AttnArgs* ap = &a;
+    AttnArgs lds_args;
+    if (in_lds && a.att_g) {  // the scores fit: keep them in LDS
+        lds_args = a;
+        lds_args.att_g = nullptr;
+        ap = &lds_args;
+    }
+    const size_t lds = attention_lds(a.head_dim, a.seq, in_lds);
+    if (a.head_dim == 64) return launch_attention<64>(*ap, lds, stream);
+    if (a.head_dim == 128) return launch_attention<128>(*ap, lds, stream);
+    return launch_attention<0>(*ap, lds, stream);
 }
 
 hipError_t argmax_advance(const float* logits, int vocab, uint32_t* tokens, int* pos, int prompt_len, int total,

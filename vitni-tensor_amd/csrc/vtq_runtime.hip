@@ -203,7 +203,7 @@ struct vtqrt_model {
     // device state of a run: activations, KV cache, tokens, position
     float *x = nullptr, *xb = nullptr, *qkv = nullptr, *att = nullptr, *ffn = nullptr, *gate = nullptr,
           *up = nullptr, *tmp = nullptr, *logits = nullptr, *kc = nullptr, *vc = nullptr, *hist = nullptr,
-          *rope = nullptr;
+          *rope = nullptr, *att_g = nullptr;  // att_g: score rows of contexts too long for LDS
     size_t hist_cap = 0;
     uint32_t* tokens = nullptr;
     int* pos = nullptr;
@@ -320,6 +320,7 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
         a.seq = m->seq;
         a.theta = m->theta;
         a.neox = m->neox ? 1 : 0;
+        a.att_g = m->att_g;
         if ((rc = hip_check(m, dec::attention(a, m->stream), "attention"))) break;
         // x = x + Wo att
         if (fused_args(m, regime, vtq::kEpiAccumulate, {&Ly.wo}, {dim}, nullptr, dim, &fa, &type)) {
@@ -432,6 +433,7 @@ int enqueue_step_recorded(vtqrt_model* m, int regime, int prompt_len, int total,
         a.seq = m->seq;
         a.theta = m->theta;
         a.neox = m->neox ? 1 : 0;
+        a.att_g = m->att_g;
         if ((rc = hip_check(m, dec::attention(a, m->stream), "attention"))) break;
         if ((rc = linear(m, regime, Ly.wo, R[RecSlots::ATT], dim, dim, R[RecSlots::XB2])) ||
             (rc = hip_check(m, dec::add_inplace(m->x, R[RecSlots::XB2], dim, m->stream), "residual")) ||
@@ -619,7 +621,7 @@ void vtqrt_free(vtqrt_model* m) {
     if (m->stream) (void)hipStreamSynchronize(m->stream);
     for (void* p : {(void*)m->dblob, (void*)m->x, (void*)m->xb, (void*)m->qkv, (void*)m->att, (void*)m->ffn,
                     (void*)m->gate, (void*)m->up, (void*)m->tmp, (void*)m->logits, (void*)m->kc, (void*)m->vc,
-                    (void*)m->hist, (void*)m->tokens, (void*)m->pos, (void*)m->rope})
+                    (void*)m->hist, (void*)m->tokens, (void*)m->pos, (void*)m->rope, (void*)m->att_g})
         if (p) (void)hipFree(p);
     if (m->rec_dev) (void)hipFree(m->rec_dev);
     if (m->rec_host) (void)hipHostFree(m->rec_host);
@@ -754,6 +756,11 @@ int vtqrt_load(int device, const uint8_t* gguf, size_t len, vtqrt_model** out) {
         (rc = dalloc(&m->kc, kv_elems)) || (rc = dalloc(&m->vc, kv_elems)) ||
         (rc = dalloc(&m->tokens, (size_t)m->seq + 1)) || (rc = dalloc(&m->pos, 1)) || (rc = dalloc(&m->rope, head)))
         return rc;
+    // a context too long for the attention kernel's LDS keeps each head's
+    // scores in a row of HBM
+    if (head > 0 && m->dim % m->heads == 0 && !vtq::decode::attention_scores_in_lds(head, m->seq) &&
+        (rc = dalloc(&m->att_g, (size_t)m->heads * (((size_t)m->seq + 3) & ~(size_t)3))))
+        return rc;
     return VTQ_OK;
 }
 
@@ -839,7 +846,7 @@ int run_impl(vtqrt_model* m, int regime, const char* model_id, const uint8_t wei
     const int head = m->dim / m->heads;
     if (head % 2) return fail(m, VTQ_E_NOT_IMPLEMENTED, "vtq: odd head dimension (RoPE pairs)");
     if (!vtq::decode::attention_supported(head, m->seq))
-        return fail(m, VTQ_E_NOT_IMPLEMENTED, "vtq: head dimension or context length beyond the attention kernel");
+        return fail(m, VTQ_E_NOT_IMPLEMENTED, "vtq: head dimension beyond the attention kernel");
     if (m->dim > 32768) return fail(m, VTQ_E_NOT_IMPLEMENTED, "vtq: model dimension above 32768 (rms_norm)");
     const uint32_t rows = table_rows(m);
     if ((rc = hip_check(m, hipSetDevice(m->device), "hipSetDevice"))) return rc;
