@@ -439,9 +439,10 @@ __global__ __launch_bounds__(64 * (PcWin<Dec, CPW>::NPW + 1)) void canon_pc_kern
 //                   row r block b at 4(8r + b)
 // Producer wave p (1..4) issues the loads of part p-1 of every window in
 // window order, so before window w it waits for vmcnt(nwin - 1 - w) of its
-// own loads, and the barrier that follows makes the window visible to all.
-// Eight producer waves (waves 5..8 issue no loads) each form 4 products per
-// lane and window.
+// own loads, and the barrier that follows makes the window visible to all;
+// it keeps one window more than the step needs visible, so the producers
+// read each window's inputs a step ahead.  Eight producer waves (waves 5..8
+// issue no loads) each form 4 products per lane and window.
 // Products (x_i * w_i with w_i = d * q_i, exact in binary32) go to a
 // double-buffered chain-major buffer; the consumer wave adds them to its 64
 // chains (8 rows x 8 lanes) in the reference's order, as canon_pc_kernel.
@@ -542,8 +543,8 @@ __global__ __launch_bounds__(576) void q8_lds_kernel(const float* __restrict__ x
             else load_to_lds<4>(rw, off + 272u * w, dst);
         }
     }
-    // window 0 in LDS
-    if (wave > 0 && wave <= 4) wait_vmcnt<NWIN - 1>();
+    // windows 0 and 1 in LDS (the producers read each window one step ahead)
+    if (wave > 0 && wave <= 4) wait_vmcnt<NWIN >= 2 ? NWIN - 2 : 0>();
     __syncthreads();
     if (wave == 0) {
         // consumer: lane = row r (lane / 8), chain j (lane % 8)
@@ -571,25 +572,37 @@ __global__ __launch_bounds__(576) void q8_lds_kernel(const float* __restrict__ x
     }
     // producers: lane L -> row r, block b of the window, elements k .. k+3 of the block
     // (chains k % 8 .. k % 8 + 3, position 4b + k / 8)
+    // Each window's codes, scale and x are read into registers one step
+    // ahead (the loader waves keep two windows visible), so a step's reads
+    // run under the previous step's products and barrier.
     const int L = tid - 64, r = L >> 6, b = (L >> 3) & 7, k = 4 * (L & 7);
     float* const pdst0 = prod + r * 8 * kQ8ChainStride + (4 * b + (k >> 3)) + (k & 7) * kQ8ChainStride;
+    uint32_t cq, dh;
+    float4 x0;
+    auto read_window = [&](int w) __attribute__((always_inline)) {
+        const uint8_t* wb = win + w * kQ8WinBytes;
+        cq = *reinterpret_cast<const uint32_t*>(wb + r * 256 + b * 32 + k);
+        dh = *reinterpret_cast<const uint16_t*>(wb + 3072 + 4 * (8 * r + b));
+        x0 = *reinterpret_cast<const float4*>(wb + 2048 + 4 * (32 * b + k));
+    };
+    read_window(0);
 #pragma unroll
     for (int s = 0; s <= NWIN; s++) {
         if (s < NWIN) {
-            const uint8_t* wb = win + s * kQ8WinBytes;
-            const uint32_t cq = *reinterpret_cast<const uint32_t*>(wb + r * 256 + b * 32 + k);
-            const float d = f16_hw(*reinterpret_cast<const uint16_t*>(wb + 3072 + 4 * (8 * r + b)));
-            const float4 x0 = *reinterpret_cast<const float4*>(wb + 2048 + 4 * (32 * b + k));
+            const uint32_t cq_s = cq;
+            const float d = f16_hw(dh);
             const float xa[4] = {x0.x, x0.y, x0.z, x0.w};
+            if (s + 1 < NWIN) read_window(s + 1);  // visible since the previous barrier
             float* pd = pdst0 + (s & 1) * (8 * 8 * kQ8ChainStride);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int q = (int)(int8_t)(uint8_t)(cq >> (8 * i));
+                const int q = (int)(int8_t)(uint8_t)(cq_s >> (8 * i));
                 const float wv = d * (float)q;  // exact: an f16 times an int8
                 pd[i * kQ8ChainStride] = xa[i] * wv;
             }
         }
-        if (s + 1 < NWIN && wave <= 4) wait_vmcnt_upto15(NWIN - 2 - s);
+        // window s + 2 in LDS before the barrier that ends step s
+        if (s + 2 < NWIN && wave <= 4) wait_vmcnt_upto15(NWIN - 3 - s);
         __syncthreads();
     }
 }
