@@ -87,7 +87,8 @@ const char *vtq_last_error(const vtq_ctx *ctx);
 /* Library version string, "vtq <major>.<minor>.<patch> (gfx950)".  It names
  * the ABI of this header and of vtq_runtime.h together; 0.2.0 added the
  * trailing digest_v1 argument of vtqrt_run (a caller built against 0.1.0
- * headers must not load this library). */
+ * headers must not load this library); 0.3.0 added vtqrt_set_prompt_mode
+ * (no existing signature changed). */
 const char *vtq_version(void);
 
 /* ---- host-pointer entry points (synchronous; y is complete on return) ----

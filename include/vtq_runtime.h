@@ -99,6 +99,21 @@ int vtqrt_run(vtqrt_model *m, int regime, const char *model_id, const uint8_t we
               const uint32_t *prompt, int prompt_len, int n_new, float *logits, uint32_t *tokens,
               uint8_t digest[32], uint8_t digest_v1[32]);
 
+/* How vtqrt_run processes the prompt.  VTQRT_PROMPT_BATCHED (the default):
+ * positions 0 .. prompt_len-1 in one pass, every linear over all prompt
+ * rows at once (the prefill GEMM for Q4_K), then the decode steps from
+ * position prompt_len; where a position's scores do not fit in LDS, or with
+ * a one-token prompt, it steps as below.  VTQRT_PROMPT_STEPWISE: one
+ * forward_quantized::step per position, as run_quantized's loop
+ * (src/model/inference.rs:313-329).  Both give the same tokens, digests and
+ * logits bit for bit: the reference's batch rows are independent, and each
+ * position's norm, cache write and attention are its own step's.
+ * vtqrt_run_recorded always steps.  No counterpart in the reference (its
+ * loop only steps); added in ABI 0.3.0. */
+#define VTQRT_PROMPT_BATCHED 0
+#define VTQRT_PROMPT_STEPWISE 1
+int vtqrt_set_prompt_mode(vtqrt_model *m, int mode);
+
 /* run_quantized with a PerOpRecorder and/or a PerActivationRecorder attached
  * to every step (src/model/forward_quantized.rs:64-132, :260-284,
  * step_with_recorders :329-655): per op, BLAKE3 of its f32 input and output

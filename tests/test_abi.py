@@ -22,8 +22,9 @@ def declared_functions():
 def test_library_built_and_loads():
     assert os.path.exists(vtq.LIB_PATH), "run __graft_entry__.build()"
     lib = vtq.load_library()
-    # 0.2.0: vtqrt_run takes the trailing digest_v1 argument (include/vtq.h)
-    assert lib.vtq_version().decode().startswith("vtq 0.2.")
+    # 0.2.0: vtqrt_run takes the trailing digest_v1 argument; 0.3.0 adds
+    # vtqrt_set_prompt_mode (include/vtq.h)
+    assert lib.vtq_version().decode().startswith("vtq 0.3.")
 
 
 def test_every_declared_symbol_is_exported():

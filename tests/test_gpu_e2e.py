@@ -3,7 +3,8 @@
 libvtq_runtime (every linear on the GPU through libvtq) must reproduce the
 oracle's restatement of inference::run_quantized (src/model/inference.rs:
 274-345) bit for bit: the logits of every decode step, the generated tokens
-and the vitnify-receipt v2 digest, in both Q4_K regimes.
+and the vitnify-receipt v2 digest, in both Q4_K regimes, with the prompt
+taken in one batched pass (the runtime's default) and step by step.
 """
 import numpy as np
 import pytest
@@ -41,14 +42,20 @@ def compare(cfg, prompt_len, n_new, regimes=(0, 1), threads=8, **variant):
     try:
         for regime in regimes:
             t_o, d_o, l_o = om.run(prompt, n_new, wh_o, regime=regime, threads=threads)
-            t_g, d_g, l_g = gm.run(prompt, n_new, wh_p, regime=regime)
-            assert l_g.shape == l_o.shape
-            bad = np.nonzero((l_g.view(np.uint32) != l_o.view(np.uint32)).any(axis=1))[0]
-            assert bad.size == 0, f"regime {regime}: logits differ first at step {bad[0]}"
-            assert np.array_equal(t_g, t_o), f"regime {regime}: tokens {t_g} vs {t_o}"
-            assert d_g == d_o, f"regime {regime}: digest {d_g} vs {d_o}"
-            # compute_digest_v1 of the same cert (vitni-receipt's model_digest_v1)
-            assert gm.digest_v1 == om.digest_v1 != d_o
+            for stepwise in (False, True):
+                mode = f"regime {regime}, {'stepwise' if stepwise else 'batched'} prompt"
+                t_g, d_g, l_g = gm.run(prompt, n_new, wh_p, regime=regime, stepwise=stepwise)
+                assert l_g.shape == l_o.shape
+                bad = np.nonzero((l_g.view(np.uint32) != l_o.view(np.uint32)).any(axis=1))[0]
+                assert bad.size == 0, f"{mode}: logits differ first at step {bad[0]}"
+                assert np.array_equal(t_g, t_o), f"{mode}: tokens {t_g} vs {t_o}"
+                assert d_g == d_o, f"{mode}: digest {d_g} vs {d_o}"
+                # compute_digest_v1 of the same cert (vitni-receipt's model_digest_v1)
+                assert gm.digest_v1 == om.digest_v1 != d_o
+                # without the logits history the batched pass computes only
+                # the last prompt position's logits
+                t_n, d_n, _ = gm.run(prompt, n_new, wh_p, regime=regime, stepwise=stepwise, want_logits=False)
+                assert np.array_equal(t_n, t_o) and d_n == d_o, f"{mode}, no logits history"
     finally:
         gm.close()
     return d_o
@@ -56,6 +63,15 @@ def compare(cfg, prompt_len, n_new, regimes=(0, 1), threads=8, **variant):
 
 def test_e2e_small_both_regimes():
     compare(SMALL, 8, 8)
+
+
+def test_e2e_batched_prompt_lengths():
+    # prompts of 2 (the smallest batched pass), 31 / 32 / 33 rows (the
+    # linears switch from the batched GEMV to the prefill GEMM at 32) and a
+    # prompt with no new tokens (the pass ends at the last prompt step)
+    for p, n in ((2, 3), (31, 2), (32, 2), (33, 2), (40, 0)):
+        compare(MEDIUM, p, n, regimes=(0,))
+    compare(SMALL, 33, 4, regimes=(1,))
 
 
 def test_e2e_medium_odd_lengths():

@@ -402,7 +402,7 @@ hipError_t allow_dynamic_lds(const void* kernel, size_t bytes) {
 
 extern "C" {
 
-const char* vtq_version(void) { return "vtq 0.2.0 (gfx950)"; }
+const char* vtq_version(void) { return "vtq 0.3.0 (gfx950)"; }
 
 int vtq_create(int device, vtq_ctx** out) {
     if (!out) return VTQ_E_INVALID_ARGUMENT;

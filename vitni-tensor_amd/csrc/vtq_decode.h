@@ -34,6 +34,8 @@ hipError_t embed(int ggml_type, const uint8_t* table, uint32_t rows, const uint3
 // rms_norm_slice (src/ops/rms_norm.rs:60-110): out = x * scale * w with the
 // sum of squares accumulated serially, as the reference does.
 hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out, hipStream_t stream);
+// the same for `rows` rows of n floats (row r of x into row r of out)
+hipError_t rms_norm_rows(const float* x, const float* w, int n, int rows, float eps, float* out, hipStream_t stream);
 
 struct AttnArgs {
     const float* qkv;            // q[dim] | k[kv_dim] | v[kv_dim] of this step
@@ -48,6 +50,10 @@ struct AttnArgs {
     // the heads' score rows in HBM, [heads][seq rounded up to 4], where
     // attention_scores_in_lds is false; nullptr otherwise
     float* att_g = nullptr;
+    // 0: one decode step at *pos.  P > 0: a prompt pass over positions
+    // 0..P-1 at once (qkv, cs and out hold P rows; rope_cache_rows has
+    // written every position's k and v; the scores must fit in LDS)
+    int batched = 0;
 };
 // RoPE of q and of this step's k, the cache write of k and v at *pos, and
 // per-head softmax attention (src/model/forward_quantized.rs:405-560).
@@ -58,6 +64,13 @@ struct AttnArgs {
 bool attention_supported(int head_dim, int seq);
 bool attention_scores_in_lds(int head_dim, int seq);
 hipError_t attention(const AttnArgs& a, hipStream_t stream);
+// The prompt pass's cache write: position p's k (bias, RoPE) and v for
+// p < a.batched, as attention computes them for its own position.
+hipError_t rope_cache_rows(const AttnArgs& a, hipStream_t stream);
+// embedding_row of tokens[0..P) into x[P][dim], and position p's RoPE angles
+// into rope.cs[p * head_dim ..] (when rope.cs is set)
+hipError_t embed_rows(int ggml_type, const uint8_t* table, uint32_t rows, const uint32_t* tokens, int P, int dim,
+                      float* x, const RopeArgs& rope, hipStream_t stream);
 
 // The embedding table, for the next step's row (see embed).
 struct EmbedArgs {

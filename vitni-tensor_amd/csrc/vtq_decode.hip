@@ -115,12 +115,32 @@ __global__ __launch_bounds__(256) void embed_kernel(int type, const uint8_t* __r
     for (int i = threadIdx.x; i < dim; i += blockDim.x) x[i] = embed_elem(type, row, i);
 }
 
+// the prompt's rows at once: workgroup p embeds tokens[p] into x[p][..] and
+// writes position p's RoPE angles to cs[p * head_dim ..]
+__global__ __launch_bounds__(256) void embed_rows_kernel(int type, const uint8_t* __restrict__ table, uint32_t rows,
+                                                         const uint32_t* __restrict__ tokens, int dim, size_t rb,
+                                                         float* __restrict__ x, RopeArgs rope) {
+    const int p = (int)blockIdx.x;
+    if (rope.cs) {
+        RopeArgs rp = rope;
+        rp.cs = rope.cs + (size_t)p * rope.head_dim;
+        rope_table(rp, p);
+    }
+    const uint32_t tok = tokens[p];
+    const uint8_t* row = table + (size_t)(tok < rows ? tok : 0u) * rb;
+    float* xp = x + (size_t)p * dim;
+    for (int i = threadIdx.x; i < dim; i += blockDim.x) xp[i] = embed_elem(type, row, i);
+}
+
 // products in parallel, the sum of squares in the reference's serial order
 // by wave 0: where the walk of vtq_sumsq.h applies (1024-4096 terms, a
 // multiple of 64) with the products in its pass layout and waves 1-3 as its
 // helpers, otherwise as one chain over the products in order
 __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int n,
                                                        float eps, float* __restrict__ out) {
+    // one row per workgroup (rows of n floats, row blockIdx.x)
+    x += (size_t)blockIdx.x * n;
+    out += (size_t)blockIdx.x * n;
     extern __shared__ float4 prod4[];
     float* prod = reinterpret_cast<float*>(prod4);
     __shared__ float scale_s;
@@ -213,10 +233,16 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     // (head_dim 64) thread t's cached k row t into registers.  Rows at or
     // past the position hold older values and are never used; rows past the
     // cache are not read.
-    const int p = *a.pos;
+    // a prompt pass (a.batched positions): workgroup (h, p) reads row p of
+    // q | k | v and of the angle tables and writes row p of the output; the
+    // caller has already written every position's k and v to the cache
+    const int p = a.batched ? (int)blockIdx.y : *a.pos;
+    const float* qkv = a.batched ? a.qkv + (size_t)p * (dim + 2 * kv_dim) : a.qkv;
+    const float* cs = a.batched ? a.cs + (size_t)p * hd : a.cs;
+    float* out = a.batched ? a.out + (size_t)p * dim : a.out;
     float qv = 0.0f, kv = 0.0f, vv = 0.0f, rc = 0.0f, rs = 0.0f;
-    if (t0 < hd) qv = a.qkv[h * hd + t0], kv = a.qkv[dim + hk * hd + t0], vv = a.qkv[dim + kv_dim + hk * hd + t0];
-    if (t0 < hd / 2) rc = a.cs[2 * t0], rs = a.cs[2 * t0 + 1];
+    if (t0 < hd) qv = qkv[h * hd + t0], kv = qkv[dim + hk * hd + t0], vv = qkv[dim + kv_dim + hk * hd + t0];
+    if (t0 < hd / 2) rc = cs[2 * t0], rs = cs[2 * t0 + 1];
     constexpr int KPT = kFast ? HD / 4 : 1;
     float4 kr[KPT], vr[KPT];
     const bool fast = kFast && p < kAttnThreads;
@@ -244,8 +270,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
         }
     }
     for (int d = t0; d < hd; d += kAttnThreads) {
-        float q = d == t0 ? qv : a.qkv[h * hd + d], k = d == t0 ? kv : a.qkv[dim + hk * hd + d],
-              v = d == t0 ? vv : a.qkv[dim + kv_dim + hk * hd + d];
+        float q = d == t0 ? qv : qkv[h * hd + d], k = d == t0 ? kv : qkv[dim + hk * hd + d],
+              v = d == t0 ? vv : qkv[dim + kv_dim + hk * hd + d];
         if (a.bq) q = q + a.bq[h * hd + d];
         if (a.bk) k = k + a.bk[hk * hd + d];
         if (a.bv) v = v + a.bv[hk * hd + d];
@@ -256,7 +282,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     __syncthreads();
     // RoPE with this step's angles (rope_table)
     for (int m = t0; m < hd / 2; m += kAttnThreads) {
-        const float c = m == t0 ? rc : a.cs[2 * m], s = m == t0 ? rs : a.cs[2 * m + 1];
+        const float c = m == t0 ? rc : cs[2 * m], s = m == t0 ? rs : cs[2 * m + 1];
         const int i0 = a.neox ? m : 2 * m, i1 = a.neox ? m + hd / 2 : 2 * m + 1;
         const float q0 = qs[i0], q1 = qs[i1], k0 = kp[i0], k1 = kp[i1];
         qs[i0] = q0 * c - q1 * s;
@@ -267,7 +293,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     __syncthreads();
     // the cache write, once per KV head; other heads of the group read
     // positions < pos from the cache and this position from kp / vp
-    if (h % kv_mul == 0) {
+    if (!a.batched && h % kv_mul == 0) {
         for (int d = t0; d < hd; d += kAttnThreads) {
             a.kc[(size_t)p * kv_dim + hk * hd + d] = kp[d];
             a.vc[(size_t)p * kv_dim + hk * hd + d] = vp[d];
@@ -390,7 +416,35 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
-    if (t0 < hd) a.out[h * hd + t0] = acc + att[p] * vp[t0];
+    if (t0 < hd) out[h * hd + t0] = acc + att[p] * vp[t0];
+}
+
+// The cache write of a prompt pass: workgroup (p, hk) writes position p's
+// roped k and its v of KV head hk, computed as attention_kernel does for its
+// own position (bias, then the RoPE pairs with position p's angles).
+__global__ __launch_bounds__(kAttnThreads) void rope_cache_kernel(AttnArgs a) {
+    __shared__ float kp[kAttnThreads];
+    const int p = (int)blockIdx.x, hk = (int)blockIdx.y, hd = a.head_dim, t0 = threadIdx.x;
+    const int kv_dim = a.kv_heads * hd, dim = a.heads * hd;
+    const float* qkv = a.qkv + (size_t)p * (dim + 2 * kv_dim);
+    const float* cs = a.cs + (size_t)p * hd;
+    float* kc = a.kc + (size_t)p * kv_dim + hk * hd;
+    float* vc = a.vc + (size_t)p * kv_dim + hk * hd;
+    for (int d = t0; d < hd; d += kAttnThreads) {
+        float k = qkv[dim + hk * hd + d], v = qkv[dim + kv_dim + hk * hd + d];
+        if (a.bk) k = k + a.bk[hk * hd + d];
+        if (a.bv) v = v + a.bv[hk * hd + d];
+        kp[d] = k;
+        vc[d] = v;
+    }
+    __syncthreads();
+    for (int m = t0; m < hd / 2; m += kAttnThreads) {
+        const float c = cs[2 * m], s = cs[2 * m + 1];
+        const int i0 = a.neox ? m : 2 * m, i1 = a.neox ? m + hd / 2 : 2 * m + 1;
+        const float k0 = kp[i0], k1 = kp[i1];
+        kc[i0] = k0 * c - k1 * s;
+        kc[i1] = k0 * s + k1 * c;
+    }
 }
 
 constexpr int kArgThreads = 1024;
@@ -517,10 +571,19 @@ hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out
     return hipGetLastError();
 }
 
+hipError_t rms_norm_rows(const float* x, const float* w, int n, int rows, float eps, float* out, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    const size_t lds = sumsq_walk_head(n) ? 4096 * 4 + sizeof(SumsqWalk) : (size_t)((n + 3) & ~3) * 4;
+    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(rms_norm_kernel), lds)) return e;
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)rows), dim3(256), lds, stream, x, w, n, eps, out);
+    return hipGetLastError();
+}
+
 template <int HD>
 static hipError_t launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
     if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(attention_kernel<HD>), lds)) return e;
-    hipLaunchKernelGGL(attention_kernel<HD>, dim3((unsigned)a.heads), dim3(kAttnThreads), lds, stream, a);
+    hipLaunchKernelGGL(attention_kernel<HD>, dim3((unsigned)a.heads, (unsigned)(a.batched ? a.batched : 1)),
+                       dim3(kAttnThreads), lds, stream, a);
     return hipGetLastError();
 }
 
@@ -543,6 +606,8 @@ hipError_t attention(const AttnArgs& a, hipStream_t stream) {
     if (!attention_supported(a.head_dim, a.seq)) return hipErrorInvalidValue;
     const bool in_lds = attention_scores_in_lds(a.head_dim, a.seq);
     if (!in_lds && !a.att_g) return hipErrorInvalidValue;
+    // a prompt pass keeps every workgroup's scores in its own LDS
+    if (a.batched && (!in_lds || a.batched < 0 || a.batched > a.seq)) return hipErrorInvalidValue;
     const AttnArgs* ap = &a;
     AttnArgs lds_args;
     if (in_lds && a.att_g) {  // the scores fit: keep them in LDS
@@ -554,6 +619,21 @@ hipError_t attention(const AttnArgs& a, hipStream_t stream) {
     if (a.head_dim == 64) return launch_attention<64>(*ap, lds, stream);
     if (a.head_dim == 128) return launch_attention<128>(*ap, lds, stream);
     return launch_attention<0>(*ap, lds, stream);
+}
+
+hipError_t embed_rows(int ggml_type, const uint8_t* table, uint32_t rows, const uint32_t* tokens, int P, int dim,
+                      float* x, const RopeArgs& rope, hipStream_t stream) {
+    if (P <= 0) return hipSuccess;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)P), dim3(256), 0, stream, ggml_type, table, rows, tokens, dim,
+                       row_bytes(ggml_type, dim), x, rope);
+    return hipGetLastError();
+}
+
+hipError_t rope_cache_rows(const AttnArgs& a, hipStream_t stream) {
+    if (a.batched <= 0 || a.batched > a.seq || !attention_supported(a.head_dim, a.seq)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rope_cache_kernel, dim3((unsigned)a.batched, (unsigned)a.kv_heads), dim3(kAttnThreads), 0,
+                       stream, a);
+    return hipGetLastError();
 }
 
 hipError_t argmax_advance(const float* logits, int vocab, uint32_t* tokens, int* pos, int prompt_len, int total,

@@ -17,7 +17,9 @@
 // sequence and the step position live in device memory, so a decode step is
 // a fixed sequence of kernel launches (vtq_decode.hip for the non-linear
 // parts, libvtq for the linears) that is captured once per run in a HIP graph
-// and replayed for every position.  The host only uploads the prompt and
+// and replayed for every position past the prompt; the prompt's positions
+// run before it as one batched pass (enqueue_prefill), or step by step like
+// the rest (vtqrt_set_prompt_mode).  The host only uploads the prompt and
 // reads back the generated tokens (and the logits history, when asked for)
 // once at the end.  In the integer regime the Q4_K / Q6_K linears of a layer
 // are fused: q, k and v in one launch, the residual add into the Wo and W2
@@ -205,6 +207,10 @@ struct vtqrt_model {
           *up = nullptr, *tmp = nullptr, *logits = nullptr, *kc = nullptr, *vc = nullptr, *hist = nullptr,
           *rope = nullptr, *att_g = nullptr;  // att_g: score rows of contexts too long for LDS
     size_t hist_cap = 0;
+    // the prompt pass (all prompt positions at once): its activations, grown per run
+    float* pf = nullptr;
+    size_t pf_cap = 0;
+    int prompt_mode = VTQRT_PROMPT_BATCHED;
     uint32_t* tokens = nullptr;
     int* pos = nullptr;
     // receipts: one step's recorded tensors (device and pinned host copies),
@@ -232,11 +238,15 @@ const float* f32_at(const vtqrt_model* m, const Lin& t) {
     return t.type >= 0 ? reinterpret_cast<const float*>(m->dblob + t.dev) : nullptr;
 }
 
-// y = W x through the C ABI (any type, either regime)
-int linear(vtqrt_model* m, int regime, const Lin& w, const float* x, int in_feat, int out_feat, float* y) {
-    const int rc = vtq_linear_device(m->ctx, w.type, regime, x, m->dblob + w.dev, w.nbytes, y, 1, (size_t)in_feat,
+// y = W x through the C ABI (any type, either regime); `rows` rows of x and y
+int linear_rows(vtqrt_model* m, int regime, int type, const uint8_t* w, size_t w_len, const float* x, int rows,
+                int in_feat, int out_feat, float* y) {
+    const int rc = vtq_linear_device(m->ctx, type, regime, x, w, w_len, y, (size_t)rows, (size_t)in_feat,
                                      (size_t)out_feat, m->stream);
     return rc ? fail(m, rc, vtq_last_error(m->ctx)) : VTQ_OK;
+}
+int linear(vtqrt_model* m, int regime, const Lin& w, const float* x, int in_feat, int out_feat, float* y) {
+    return linear_rows(m, regime, w.type, m->dblob + w.dev, w.nbytes, x, 1, in_feat, out_feat, y);
 }
 
 // rows of the embedding table (embedding_row checks a row against the table's bytes)
@@ -360,6 +370,132 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
     if (rc) return rc;
     return hip_check(m, dec::argmax_advance(m->logits, m->vocab, m->tokens, m->pos, prompt_len, total, hist,
                                             embed_args(m), m->stream),
+                     "argmax");
+}
+
+// The prompt pass: positions 0 .. P-1 of forward_quantized::step at once,
+// then step P-1's argmax (which writes tokens[P], the next step's embedding
+// row and angles, and advances *pos to P).  Every linear takes the P rows as
+// one batch (the prefill GEMM for Q4_K), and batch rows are independent, so
+// each position's activations, cache rows and logits are those of its own
+// step: the same kernels' arithmetic per row (RMSNorm per row, the cache
+// write and attention of each position as the step computes them for its
+// own), in the same order.  Only step P-1's logits feed the run; with hist
+// every prompt position's logits are also computed, into hist.
+int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
+    namespace dec = vtq::decode;
+    const int dim = m->dim, head = dim / m->heads, kv_dim = m->kv_heads * head, hidden = m->hidden;
+    const int qw = dim + 2 * kv_dim;
+    auto al = [](size_t n) { return (n + 63) / 64 * 64; };
+    const size_t Pz = (size_t)P;
+    const size_t nX = al(Pz * dim), nQKV = al(Pz * qw), nH = al(Pz * hidden), nCS = al(Pz * head),
+                 nK = al(Pz * kv_dim);
+    const size_t need = 5 * nX + nQKV + 3 * nH + nCS + 2 * nK;
+    int rc = VTQ_OK;
+    if (m->pf_cap < need) {
+        if (m->pf) (void)hipFree(m->pf);
+        m->pf = nullptr;
+        m->pf_cap = 0;
+        if ((rc = hip_check(m, hipMalloc(&m->pf, need * 4), "hipMalloc(prompt pass)"))) return rc;
+        m->pf_cap = need;
+    }
+    float* X = m->pf;
+    float* XN = X + nX;
+    float* ATT = XN + nX;
+    float* TMP = ATT + nX;
+    float* QB = TMP + nX;
+    float* QKV = QB + nX;
+    float* G = QKV + nQKV;
+    float* U = G + nH;
+    float* F = U + nH;
+    float* CS = F + nH;
+    float* KB = CS + nCS;
+    float* VB = KB + nK;
+    dec::RopeArgs ra = rope_args(m);
+    ra.cs = CS;
+    if ((rc = hip_check(m, dec::embed_rows(m->tok.type, m->dblob + m->tok.dev, table_rows(m), m->tokens, P, dim, X, ra,
+                                           m->stream),
+                        "embedding_row")))
+        return rc;
+    auto cp_cols = [&](float* dst, const float* src, int width) {
+        return hip_check(m, hipMemcpy2DAsync(dst, (size_t)qw * 4, src, (size_t)width * 4, (size_t)width * 4, Pz,
+                                             hipMemcpyDeviceToDevice, m->stream),
+                         "q|k|v rows");
+    };
+    for (int l = 0; !rc && l < m->layers; l++) {
+        const Layer& Ly = m->L[l];
+        // q | k | v = W (rms_norm(x, attn_norm)), one row per position
+        rc = hip_check(m, dec::rms_norm_rows(X, f32_at(m, Ly.rms_att), dim, P, m->eps, XN, m->stream), "rms_norm");
+        if (rc) break;
+        const bool joint = Ly.wk.type == Ly.wq.type && Ly.wv.type == Ly.wq.type &&
+                           Ly.wk.dev == Ly.wq.dev + Ly.wq.nbytes && Ly.wv.dev == Ly.wk.dev + Ly.wk.nbytes;
+        if (joint) {
+            // the three matrices lie back to back in the arena: one linear of dim + 2 kv_dim rows
+            rc = linear_rows(m, regime, Ly.wq.type, m->dblob + Ly.wq.dev, Ly.wq.nbytes + Ly.wk.nbytes + Ly.wv.nbytes,
+                             XN, P, dim, qw, QKV);
+        } else {
+            rc = linear_rows(m, regime, Ly.wq.type, m->dblob + Ly.wq.dev, Ly.wq.nbytes, XN, P, dim, dim, QB);
+            if (!rc) rc = linear_rows(m, regime, Ly.wk.type, m->dblob + Ly.wk.dev, Ly.wk.nbytes, XN, P, dim, kv_dim, KB);
+            if (!rc) rc = linear_rows(m, regime, Ly.wv.type, m->dblob + Ly.wv.dev, Ly.wv.nbytes, XN, P, dim, kv_dim, VB);
+            if (!rc) rc = cp_cols(QKV, QB, dim);
+            if (!rc) rc = cp_cols(QKV + dim, KB, kv_dim);
+            if (!rc) rc = cp_cols(QKV + dim + kv_dim, VB, kv_dim);
+        }
+        if (rc) break;
+        dec::AttnArgs a;
+        a.qkv = QKV;
+        a.bq = f32_at(m, Ly.bq);
+        a.bk = f32_at(m, Ly.bk);
+        a.bv = f32_at(m, Ly.bv);
+        a.kc = m->kc + (size_t)l * m->seq * kv_dim;
+        a.vc = m->vc + (size_t)l * m->seq * kv_dim;
+        a.cs = CS;
+        a.out = ATT;
+        a.pos = m->pos;
+        a.heads = m->heads;
+        a.kv_heads = m->kv_heads;
+        a.head_dim = head;
+        a.seq = m->seq;
+        a.theta = m->theta;
+        a.neox = m->neox ? 1 : 0;
+        a.att_g = nullptr;
+        a.batched = P;
+        if ((rc = hip_check(m, dec::rope_cache_rows(a, m->stream), "kv cache")) ||
+            (rc = hip_check(m, dec::attention(a, m->stream), "attention")))
+            break;
+        // x = x + Wo att
+        rc = linear_rows(m, regime, Ly.wo.type, m->dblob + Ly.wo.dev, Ly.wo.nbytes, ATT, P, dim, dim, TMP);
+        if (!rc) rc = hip_check(m, dec::add_inplace(X, TMP, P * dim, m->stream), "residual");
+        // ffn = silu(W1 h) * (W3 h), h = rms_norm(x, ffn_norm)
+        if (!rc) rc = hip_check(m, dec::rms_norm_rows(X, f32_at(m, Ly.rms_ffn), dim, P, m->eps, XN, m->stream), "rms_norm");
+        if (!rc) rc = linear_rows(m, regime, Ly.w1.type, m->dblob + Ly.w1.dev, Ly.w1.nbytes, XN, P, dim, hidden, G);
+        if (!rc) rc = linear_rows(m, regime, Ly.w3.type, m->dblob + Ly.w3.dev, Ly.w3.nbytes, XN, P, dim, hidden, U);
+        if (!rc) rc = hip_check(m, dec::swiglu(G, U, F, P * hidden, m->stream), "swiglu");
+        // x = x + W2 ffn
+        if (!rc) rc = linear_rows(m, regime, Ly.w2.type, m->dblob + Ly.w2.dev, Ly.w2.nbytes, F, P, hidden, dim, TMP);
+        if (!rc) rc = hip_check(m, dec::add_inplace(X, TMP, P * dim, m->stream), "residual");
+    }
+    if (rc) return rc;
+    // logits = W_out (rms_norm(x, output_norm)): every position's into hist,
+    // or position P-1's alone
+    const Lin& head_w = m->shared ? m->tok : m->wcls;
+    const float* lg = m->logits;
+    if (hist) {
+        rc = hip_check(m, dec::rms_norm_rows(X, f32_at(m, m->rms_final), dim, P, m->eps, XN, m->stream), "rms_norm");
+        if (!rc) rc = linear_rows(m, regime, head_w.type, m->dblob + head_w.dev, head_w.nbytes, XN, P, dim, m->vocab, hist);
+        lg = hist + (size_t)(P - 1) * m->vocab;
+    } else {
+        rc = hip_check(m, dec::rms_norm(X + (size_t)(P - 1) * dim, f32_at(m, m->rms_final), dim, m->eps, m->xb,
+                                        m->stream),
+                       "rms_norm");
+        if (!rc) rc = linear(m, regime, head_w, m->xb, dim, m->vocab, m->logits);
+    }
+    if (rc) return rc;
+    // step P-1's argmax: tokens[P], the next step's row and angles, *pos = P
+    if ((rc = hip_check(m, hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(m->pos), P - 1, 1, m->stream),
+                        "position")))
+        return rc;
+    return hip_check(m, dec::argmax_advance(lg, m->vocab, m->tokens, m->pos, P, total, hist, embed_args(m), m->stream),
                      "argmax");
 }
 
@@ -621,7 +757,8 @@ void vtqrt_free(vtqrt_model* m) {
     if (m->stream) (void)hipStreamSynchronize(m->stream);
     for (void* p : {(void*)m->dblob, (void*)m->x, (void*)m->xb, (void*)m->qkv, (void*)m->att, (void*)m->ffn,
                     (void*)m->gate, (void*)m->up, (void*)m->tmp, (void*)m->logits, (void*)m->kc, (void*)m->vc,
-                    (void*)m->hist, (void*)m->tokens, (void*)m->pos, (void*)m->rope, (void*)m->att_g})
+                    (void*)m->hist, (void*)m->tokens, (void*)m->pos, (void*)m->rope, (void*)m->att_g,
+                    (void*)m->pf})
         if (p) (void)hipFree(p);
     if (m->rec_dev) (void)hipFree(m->rec_dev);
     if (m->rec_host) (void)hipHostFree(m->rec_host);
@@ -902,10 +1039,20 @@ int run_impl(vtqrt_model* m, int regime, const char* model_id, const uint8_t wei
         }
         if (graph) (void)hipGraphDestroy(graph);
     }
-    rc = hip_check(m, vtq::decode::embed(m->tok.type, m->dblob + m->tok.dev, table_rows(m), m->tokens, m->pos, m->dim,
-                                         m->x, rope_args(m), m->stream),
-                   "embedding_row");
-    for (int pos = 0; pos < total && !rc; pos++) {
+    // the prompt at once where the recorders are off and every position's
+    // scores fit in LDS; else step by step from position 0
+    const bool batched = !rec && m->prompt_mode == VTQRT_PROMPT_BATCHED && prompt_len >= 2 &&
+                         vtq::decode::attention_scores_in_lds(head, m->seq);
+    int pos0 = 0;
+    if (batched) {
+        rc = enqueue_prefill(m, regime, prompt_len, total, hist);
+        pos0 = prompt_len;
+    } else {
+        rc = hip_check(m, vtq::decode::embed(m->tok.type, m->dblob + m->tok.dev, table_rows(m), m->tokens, m->pos,
+                                             m->dim, m->x, rope_args(m), m->stream),
+                       "embedding_row");
+    }
+    for (int pos = pos0; pos < total && !rc; pos++) {
         rc = exec ? hip_check(m, hipGraphLaunch(exec, m->stream), "hipGraphLaunch") : enqueue();
         if (!rc && rec) {
             // this step's recorded tensors to the host, hashed there
@@ -1022,6 +1169,12 @@ int vtqrt_run(vtqrt_model* m, int regime, const char* model_id, const uint8_t we
               uint8_t digest[32], uint8_t digest_v1[32]) {
     return run_impl(m, regime, model_id, weights_hash, prompt, prompt_len, n_new, logits, tokens, digest, digest_v1,
                     nullptr);
+}
+
+int vtqrt_set_prompt_mode(vtqrt_model* m, int mode) {
+    if (!m || (mode != VTQRT_PROMPT_BATCHED && mode != VTQRT_PROMPT_STEPWISE)) return VTQ_E_INVALID_ARGUMENT;
+    m->prompt_mode = mode;
+    return VTQ_OK;
 }
 
 int vtqrt_run_recorded(vtqrt_model* m, int regime, const char* model_id, const uint8_t weights_hash[32],

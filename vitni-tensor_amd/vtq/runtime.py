@@ -42,6 +42,8 @@ def lib() -> ctypes.CDLL:
         L.vtqrt_rms_norm_device.restype = i
         L.vtqrt_transcendentals_device.argtypes = [vp, sz, vp, vp]
         L.vtqrt_transcendentals_device.restype = i
+        L.vtqrt_set_prompt_mode.argtypes = [vp, i]
+        L.vtqrt_set_prompt_mode.restype = i
         _rt = L
     return _rt
 
@@ -82,6 +84,7 @@ def transcendentals_device(x_ptr, n, y_ptr, stream=None) -> None:
         raise RuntimeError(f"vtqrt_transcendentals_device failed with status {rc}")
 
 
+PROMPT_BATCHED, PROMPT_STEPWISE = 0, 1  # vtqrt_set_prompt_mode (include/vtq_runtime.h)
 RECORD_OPS = 1
 RECORD_ACTIVATIONS = 2
 
@@ -125,9 +128,15 @@ class Model:
         lib().vtqrt_dims(self.handle, dims.ctypes.data)
         self.dim, self.hidden, self.layers, self.heads, self.kv_heads, self.vocab, self.seq_len = map(int, dims)
 
-    def run(self, prompt, n_new, weights_hash: bytes, regime=0, model_id="vitni-receipt", want_logits=True):
+    def run(self, prompt, n_new, weights_hash: bytes, regime=0, model_id="vitni-receipt", want_logits=True,
+            stepwise=False):
         """(generated tokens, v2 digest hex, logits [steps][vocab] or None);
-        digest_v1 then holds the frozen v1 digest of the same cert."""
+        digest_v1 then holds the frozen v1 digest of the same cert.  The
+        prompt goes through in one batched pass unless stepwise (one step per
+        position, run_quantized's loop); both give the same bits."""
+        rc = lib().vtqrt_set_prompt_mode(self.handle, PROMPT_STEPWISE if stepwise else PROMPT_BATCHED)
+        if rc:
+            raise error_class(rc)(lib().vtqrt_last_error(self.handle).decode())
         prompt = np.ascontiguousarray(prompt, dtype=np.uint32)
         wh = np.frombuffer(bytes(weights_hash), dtype=np.uint8).copy()
         tokens = np.zeros(max(1, n_new), dtype=np.uint32)
