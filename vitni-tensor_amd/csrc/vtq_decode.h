@@ -101,6 +101,8 @@ hipError_t add_inplace(float* x, const float* y, int n, hipStream_t stream);
 // transcendental sweep, evaluated by the device libm the step uses.
 hipError_t transcendentals(const float* x, int n, float* y, hipStream_t stream);
 hipError_t swiglu(const float* gate, const float* up, float* out, int n, hipStream_t stream);
+// the same over rows of gate | up (2 * hidden floats each) into rows of hidden
+hipError_t swiglu_rows(const float* gu, int hidden, int rows, float* out, hipStream_t stream);
 
 }  // namespace decode
 }  // namespace vtq

@@ -223,7 +223,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float* vp = kp + hd;
     float* red = vp + hd;
     float* att_l = red + kAttnThreads + (4 - (3 * hd) % 4) % 4;  // 16-byte aligned for float4 reads
-    const size_t seq4 = ((size_t)a.seq + 3) & ~(size_t)3;
+    // scores held: the whole cache's, or a prompt pass's positions
+    const size_t seq4 = ((size_t)(a.batched ? a.batched : a.seq) + 3) & ~(size_t)3;
     float* att = a.att_g ? a.att_g + (size_t)h * seq4 : att_l;
     float* vt = a.att_g ? att_l : att_l + seq4;
     const int t0 = threadIdx.x;
@@ -398,7 +399,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float acc = 0.0f;
     if (fast) {
 #pragma unroll
-        for (int u = 0; u < KPT; u++) reinterpret_cast<float4*>(vt)[t0 + kAttnThreads * u] = vr[u];
+        for (int u = 0; u < KPT; u++)
+            if (t0 + kAttnThreads * u < p * (HD / 4)) reinterpret_cast<float4*>(vt)[t0 + kAttnThreads * u] = vr[u];
         __syncthreads();
         accumulate(acc, 0, p);
     } else {
@@ -544,6 +546,16 @@ __global__ void swiglu_kernel(const float* __restrict__ gate, const float* __res
     }
 }
 
+// rows of gate | up (2 * hidden floats each): out[p][j] = silu(gate) * up
+__global__ void swiglu_rows_kernel(const float* __restrict__ gu, int hidden, int rows, float* __restrict__ out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)rows * hidden) return;
+    const size_t p = i / (size_t)hidden, j = i % (size_t)hidden;
+    const float g = gu[p * 2 * hidden + j];
+    const float silu = g / (1.0f + libm::expf(-g));
+    out[i] = silu * gu[p * 2 * hidden + hidden + j];
+}
+
 }  // namespace
 
 size_t embed_row_bytes(int ggml_type, int dim) {
@@ -593,6 +605,14 @@ static size_t attention_lds(int head_dim, int seq, bool scores) {
             kAttnTile * 64) * 4;
 }
 
+// a prompt pass of P positions: P scores, and P cached v rows where the
+// head-dim-64 path holds them all (else the tiles)
+static size_t attention_lds_rows(int head_dim, int P) {
+    const bool fast = head_dim == 64 && P <= kAttnThreads;
+    return ((size_t)3 * head_dim + kAttnThreads + 4 + (((size_t)P + 3) & ~(size_t)3) +
+            (fast ? (size_t)P * head_dim : (size_t)kAttnTile * 64)) * 4;
+}
+
 bool attention_supported(int head_dim, int seq) {
     return head_dim > 0 && head_dim <= kAttnThreads && head_dim % 4 == 0 && (kAttnTile * 64) % head_dim == 0 &&
            seq > 0;
@@ -615,7 +635,7 @@ hipError_t attention(const AttnArgs& a, hipStream_t stream) {
         lds_args.att_g = nullptr;
         ap = &lds_args;
     }
-    const size_t lds = attention_lds(a.head_dim, a.seq, in_lds);
+    const size_t lds = a.batched ? attention_lds_rows(a.head_dim, a.batched) : attention_lds(a.head_dim, a.seq, in_lds);
     if (a.head_dim == 64) return launch_attention<64>(*ap, lds, stream);
     if (a.head_dim == 128) return launch_attention<128>(*ap, lds, stream);
     return launch_attention<0>(*ap, lds, stream);
@@ -670,6 +690,14 @@ hipError_t transcendentals(const float* x, int n, float* y, hipStream_t stream) 
 
 hipError_t add_inplace(float* x, const float* y, int n, hipStream_t stream) {
     hipLaunchKernelGGL(add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t swiglu_rows(const float* gu, int hidden, int rows, float* out, hipStream_t stream) {
+    const size_t n = (size_t)hidden * rows;
+    if (n == 0) return hipSuccess;
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, gu, hidden, rows,
+                       out);
     return hipGetLastError();
 }
 

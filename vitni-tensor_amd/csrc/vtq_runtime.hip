@@ -468,9 +468,16 @@ int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
         if (!rc) rc = hip_check(m, dec::add_inplace(X, TMP, P * dim, m->stream), "residual");
         // ffn = silu(W1 h) * (W3 h), h = rms_norm(x, ffn_norm)
         if (!rc) rc = hip_check(m, dec::rms_norm_rows(X, f32_at(m, Ly.rms_ffn), dim, P, m->eps, XN, m->stream), "rms_norm");
-        if (!rc) rc = linear_rows(m, regime, Ly.w1.type, m->dblob + Ly.w1.dev, Ly.w1.nbytes, XN, P, dim, hidden, G);
-        if (!rc) rc = linear_rows(m, regime, Ly.w3.type, m->dblob + Ly.w3.dev, Ly.w3.nbytes, XN, P, dim, hidden, U);
-        if (!rc) rc = hip_check(m, dec::swiglu(G, U, F, P * hidden, m->stream), "swiglu");
+        if (!rc && Ly.w3.type == Ly.w1.type && Ly.w3.dev == Ly.w1.dev + Ly.w1.nbytes) {
+            // gate | up rows from one linear of 2 * hidden rows (G and U back to back)
+            rc = linear_rows(m, regime, Ly.w1.type, m->dblob + Ly.w1.dev, Ly.w1.nbytes + Ly.w3.nbytes, XN, P, dim,
+                             2 * hidden, G);
+            if (!rc) rc = hip_check(m, dec::swiglu_rows(G, hidden, P, F, m->stream), "swiglu");
+        } else if (!rc) {
+            rc = linear_rows(m, regime, Ly.w1.type, m->dblob + Ly.w1.dev, Ly.w1.nbytes, XN, P, dim, hidden, G);
+            if (!rc) rc = linear_rows(m, regime, Ly.w3.type, m->dblob + Ly.w3.dev, Ly.w3.nbytes, XN, P, dim, hidden, U);
+            if (!rc) rc = hip_check(m, dec::swiglu(G, U, F, P * hidden, m->stream), "swiglu");
+        }
         // x = x + W2 ffn
         if (!rc) rc = linear_rows(m, regime, Ly.w2.type, m->dblob + Ly.w2.dev, Ly.w2.nbytes, F, P, hidden, dim, TMP);
         if (!rc) rc = hip_check(m, dec::add_inplace(X, TMP, P * dim, m->stream), "residual");
@@ -840,9 +847,10 @@ int vtqrt_load(int device, const uint8_t* gguf, size_t len, vtqrt_model** out) {
         place_t(V.wk, &Ly.wk);
         place_t(V.wv, &Ly.wv);
         place_t(V.wo, &Ly.wo);
+        // w1 then w3: back to back, the prompt pass runs them as one linear
         place_t(V.w1, &Ly.w1);
-        place_t(V.w2, &Ly.w2);
         place_t(V.w3, &Ly.w3);
+        place_t(V.w2, &Ly.w2);
         place(V.bq, (size_t)m->dim * 4, &Ly.bq);
         place(V.bk, (size_t)kv_dim * 4, &Ly.bk);
         place(V.bv, (size_t)kv_dim * 4, &Ly.bv);
