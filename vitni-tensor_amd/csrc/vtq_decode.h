@@ -37,6 +37,19 @@ hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out
 // the same for `rows` rows of n floats (row r of x into row r of out)
 hipError_t rms_norm_rows(const float* x, const float* w, int n, int rows, float eps, float* out, hipStream_t stream);
 
+// Byte ranges later kernels of the step read, streamed through the
+// memory-side cache by `groups` extra workgroups of the attention launch
+// (which leaves most CUs idle), so that those kernels read them from the
+// cache.  The loaded bytes are folded into one value, stored to sink only if
+// it equals magic, so the loads are kept and nothing is written in practice.
+struct Prefetch {
+    const uint8_t* p[4] = {nullptr, nullptr, nullptr, nullptr};
+    uint32_t n[4] = {0, 0, 0, 0};
+    int groups = 0;
+    uint32_t magic = 0;
+    uint32_t* sink = nullptr;
+};
+
 struct AttnArgs {
     const float* qkv;            // q[dim] | k[kv_dim] | v[kv_dim] of this step
     const float *bq, *bk, *bv;   // optional biases (added before RoPE / the cache write)
@@ -54,6 +67,7 @@ struct AttnArgs {
     // 0..P-1 at once (qkv, cs and out hold P rows; rope_cache_rows has
     // written every position's k and v; the scores must fit in LDS)
     int batched = 0;
+    Prefetch pf;  // extra workgroups (one-step launches only)
 };
 // RoPE of q and of this step's k, the cache write of k and v at *pos, and
 // per-head softmax attention (src/model/forward_quantized.rs:405-560).

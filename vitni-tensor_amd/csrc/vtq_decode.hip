@@ -186,6 +186,31 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * scale * w[i];
 }
 
+// A prefetch workgroup: workgroup g of G streams its share of every range
+// (16-byte loads, four in flight per thread).
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+__device__ void prefetch_ranges(const Prefetch& pf, int g, int G) {
+    uint32_t acc = 0;
+    const uint32_t step = (uint32_t)G * blockDim.x * 16u;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        if (!pf.n[r]) continue;
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(pf.p[r]), (short)0, (int)pf.n[r], 0x00020000);
+        for (uint32_t off = ((uint32_t)g * blockDim.x + threadIdx.x) * 16u; off < pf.n[r]; off += 4 * step) {
+            uint32_t o[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) o[u] = off + (uint32_t)u * step;  // out of range: zeros, no traffic
+            v4u v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = __builtin_bit_cast(v4u, __builtin_amdgcn_raw_buffer_load_b128(rs, o[u], 0, 0));
+#pragma unroll
+            for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        }
+    }
+    if (acc == pf.magic && pf.sink) pf.sink[0] = acc;
+}
+
 constexpr int kAttnThreads = 256;
 constexpr int kAttnTile = 256;  // cached v positions per LDS tile at head_dim 64 (64 KiB)
 
@@ -214,6 +239,10 @@ __device__ float block_max(float m, float* red) {
 // scores.
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
+    if ((int)blockIdx.x >= a.heads) {  // a prefetch workgroup
+        prefetch_ranges(a.pf, (int)blockIdx.x - a.heads, a.pf.groups);
+        return;
+    }
     extern __shared__ float4 sh4[];
     float* sh = reinterpret_cast<float*>(sh4);
     const int hd = HD > 0 ? HD : a.head_dim, h = blockIdx.x, kv_mul = a.heads / a.kv_heads, hk = h / kv_mul;
@@ -594,7 +623,8 @@ hipError_t rms_norm_rows(const float* x, const float* w, int n, int rows, float 
 template <int HD>
 static hipError_t launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
     if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(attention_kernel<HD>), lds)) return e;
-    hipLaunchKernelGGL(attention_kernel<HD>, dim3((unsigned)a.heads, (unsigned)(a.batched ? a.batched : 1)),
+    const int extra = a.batched ? 0 : a.pf.groups;
+    hipLaunchKernelGGL(attention_kernel<HD>, dim3((unsigned)(a.heads + extra), (unsigned)(a.batched ? a.batched : 1)),
                        dim3(kAttnThreads), lds, stream, a);
     return hipGetLastError();
 }

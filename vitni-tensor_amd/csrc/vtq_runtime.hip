@@ -211,6 +211,7 @@ struct vtqrt_model {
     float* pf = nullptr;
     size_t pf_cap = 0;
     int prompt_mode = VTQRT_PROMPT_BATCHED;
+    uint32_t* pf_sink = nullptr;  // the prefetch workgroups' never-taken store
     uint32_t* tokens = nullptr;
     int* pos = nullptr;
     // receipts: one step's recorded tensors (device and pinned host copies),
@@ -293,6 +294,16 @@ vtq::decode::EmbedArgs embed_args(vtqrt_model* m) {
                                   vtq::decode::embed_row_bytes(m->tok.type, m->dim), m->dim, m->x, rope_args(m)};
 }
 
+// a range for the attention launch's prefetch workgroups (at most four)
+void pf_add(vtq::decode::Prefetch& pf, const uint8_t* p, size_t n) {
+    for (int r = 0; r < 4; r++)
+        if (!pf.n[r]) {
+            pf.p[r] = p;
+            pf.n[r] = (uint32_t)std::min<size_t>(n, (size_t)1 << 31);
+            return;
+        }
+}
+
 // One decode step at position *m->pos (forward_quantized::step), enqueued
 // on m->stream.  x holds the step's embedding row on entry (the previous
 // step's argmax kernel, or the run's first embedding, wrote it).
@@ -331,6 +342,30 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
         a.theta = m->theta;
         a.neox = m->neox ? 1 : 0;
         a.att_g = m->att_g;
+        {
+            // The attention launch uses one workgroup per head and leaves the
+            // other CUs idle: one extra workgroup on each streams the weights
+            // the layer reads next (Wo, W1 | W3, the next layer's q | k | v)
+            // through the memory-side cache, so those GEMVs find them there.
+            dec::Prefetch& pf = a.pf;
+            pf.magic = 0xA5A5A5A5u;
+            pf.sink = m->pf_sink;
+            pf_add(pf, m->dblob + Ly.wo.dev, Ly.wo.nbytes);
+            if (Ly.w3.dev == Ly.w1.dev + Ly.w1.nbytes) {
+                pf_add(pf, m->dblob + Ly.w1.dev, Ly.w1.nbytes + Ly.w3.nbytes);
+            } else {
+                pf_add(pf, m->dblob + Ly.w1.dev, Ly.w1.nbytes);
+                pf_add(pf, m->dblob + Ly.w3.dev, Ly.w3.nbytes);
+            }
+            if (l + 1 < m->layers) {
+                const Layer& Ln = m->L[l + 1];
+                if (Ln.wk.dev == Ln.wq.dev + Ln.wq.nbytes && Ln.wv.dev == Ln.wk.dev + Ln.wk.nbytes)
+                    pf_add(pf, m->dblob + Ln.wq.dev, Ln.wq.nbytes + Ln.wk.nbytes + Ln.wv.nbytes);
+                else
+                    pf_add(pf, m->dblob + Ln.wq.dev, Ln.wq.nbytes);
+            }
+            pf.groups = std::max(0, m->num_cus - m->heads);
+        }
         if ((rc = hip_check(m, dec::attention(a, m->stream), "attention"))) break;
         // x = x + Wo att
         if (fused_args(m, regime, vtq::kEpiAccumulate, {&Ly.wo}, {dim}, nullptr, dim, &fa, &type)) {
@@ -765,7 +800,7 @@ void vtqrt_free(vtqrt_model* m) {
     for (void* p : {(void*)m->dblob, (void*)m->x, (void*)m->xb, (void*)m->qkv, (void*)m->att, (void*)m->ffn,
                     (void*)m->gate, (void*)m->up, (void*)m->tmp, (void*)m->logits, (void*)m->kc, (void*)m->vc,
                     (void*)m->hist, (void*)m->tokens, (void*)m->pos, (void*)m->rope, (void*)m->att_g,
-                    (void*)m->pf})
+                    (void*)m->pf, (void*)m->pf_sink})
         if (p) (void)hipFree(p);
     if (m->rec_dev) (void)hipFree(m->rec_dev);
     if (m->rec_host) (void)hipHostFree(m->rec_host);
@@ -899,7 +934,8 @@ int vtqrt_load(int device, const uint8_t* gguf, size_t len, vtqrt_model** out) {
         (rc = dalloc(&m->att, m->dim)) || (rc = dalloc(&m->ffn, m->hidden)) || (rc = dalloc(&m->gate, m->hidden)) ||
         (rc = dalloc(&m->up, m->hidden)) || (rc = dalloc(&m->tmp, m->dim)) || (rc = dalloc(&m->logits, m->vocab)) ||
         (rc = dalloc(&m->kc, kv_elems)) || (rc = dalloc(&m->vc, kv_elems)) ||
-        (rc = dalloc(&m->tokens, (size_t)m->seq + 1)) || (rc = dalloc(&m->pos, 1)) || (rc = dalloc(&m->rope, head)))
+        (rc = dalloc(&m->tokens, (size_t)m->seq + 1)) || (rc = dalloc(&m->pos, 1)) || (rc = dalloc(&m->rope, head)) ||
+        (rc = dalloc(&m->pf_sink, 64)))
         return rc;
     // a context too long for the attention kernel's LDS keeps each head's
     // scores in a row of HBM
