@@ -107,13 +107,24 @@ def test_q4k_prefill_gemm(ctx, batch, in_f, out_f):
     check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
 
 
-# rows of at most 16 super-blocks take the per-wave GEMM (32 rows x 64 tokens
-# per wave, 128-row workgroups): every row length 1..16 (each tree shape of
-# its counter), token counts either side of the 32- and 64-token tiles, row
-# counts either side of the 32-row tiles and the 128-row workgroups
+# rows of at most 16 super-blocks take the per-wave GEMM (32 rows per wave,
+# 128-row workgroups; one 32-token tile per wave at these grid sizes): every
+# row length 1..16 (each tree shape of its counter), token counts either side
+# of the 32- and 64-token tiles, row counts either side of the 32-row tiles
+# and the 128-row workgroups
 PW_SHAPES = [(32, 256, 129), (64, 512, 1), (33, 768, 129), (65, 1024, 300), (96, 1280, 128), (97, 1536, 513),
              (127, 1792, 31), (128, 2048, 130), (34, 2304, 64), (200, 2560, 257), (70, 2816, 77),
              (160, 3072, 96), (129, 3328, 33), (95, 3584, 200), (63, 3840, 127), (192, 4096, 255)]
+# grids of at least 512 workgroups take two 32-token tiles per wave: an odd
+# tile count (the last wave's second tile repeats the last one) and ragged rows
+PW2_SHAPES = [(272, 768, 13312), (300, 256, 13313), (512, 1024, 13000)]
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", PW2_SHAPES)
+def test_q4k_prefill_gemm_two_tiles_per_wave(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 11 + out_f)
+    x = synth.activations(batch * in_f, seed=in_f * 19 + batch)
+    check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
 
 
 @pytest.mark.parametrize("batch,in_f,out_f", PW_SHAPES)

@@ -22,8 +22,8 @@
 //
 // Two kernels share the activation pre-pass, which writes the token codes in
 // the MFMA operand order:
-//  * q4k_gemm_pw_kernel (rows of at most 16 super-blocks, in_feat <= 4096):
-//    each wave forms its own weight operands in registers, no barriers;
+//  * q4k_gemm_pw_kernel (rows of at most 16 super-blocks): each wave forms
+//    its own weight operands in registers, no barriers;
 //  * q4k_gemm_kernel (longer rows): a workgroup of 4 waves owns 32 weight
 //    rows x 128 tokens and builds the weight operands once per super-block
 //    in LDS.
@@ -323,7 +323,8 @@ __global__ __launch_bounds__(256, 2) void q4k_gemm_kernel(const uint8_t* __restr
 // ------------------------------------------- per-wave operand formation
 
 // Rows of at most 16 super-blocks (in_feat <= 4096).  Each wave owns 32
-// weight rows x 64 tokens (two 32-token tiles) and forms the split weight
+// weight rows x 64 tokens (two 32-token tiles; one tile where two would
+// leave the CUs idle) and forms the split weight
 // operands of its rows in registers, straight from the 144-byte blocks: no
 // LDS operand buffers and no workgroup barrier, so the two waves sharing a
 // SIMD drift out of phase and one's MFMAs run beside the other's epilogue.
@@ -348,10 +349,15 @@ __global__ __launch_bounds__(256, 2) void q4k_gemm_kernel(const uint8_t* __restr
 // 3 in the wave's own LDS (each written and read a few times per row); at
 // the last super-block the counter folds straight into the result, so level
 // 4 (R = 16) is never stored.
+//
+// Template parameter NT: token tiles per wave (2; 1 where two would leave
+// fewer than two workgroups per CU, as at prompt-sized batches).
 constexpr int kPwWaves = 4;
-constexpr int kPwLevelBytes = 2 * 4 * 64 * 16;                 // one tree level of both tiles
-constexpr int kPwLdsPerWave = 2 * kPwLevelBytes + 2 * 32 * 4;  // levels 2 and 3, then d and dmin of the rows
 constexpr int kPwMaxR = 16;
+__host__ __device__ constexpr int pw_level_bytes(int NT) { return NT * 4 * 64 * 16; }  // one tree level of NT tiles
+__host__ __device__ constexpr int pw_lds_per_wave(int NT) {
+    return 2 * pw_level_bytes(NT) + 2 * 32 * 4;  // levels 2 and 3, then d and dmin of the rows
+}
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -367,14 +373,16 @@ __device__ __forceinline__ uint32_t pk_f16(uint32_t a, uint32_t b) {  // two sma
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz((float)a, (float)b));
 }
 
+template <int NT>
 __global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uint8_t* __restrict__ W, GemmWs ws,
                                                                        float* __restrict__ y, int R, int N, int M,
                                                                        int NG, int TP) {
-    constexpr int NT = 2, D = 4, NW = kPwWaves;  // tiles per wave, k-steps of token operands in flight
+    constexpr int D = 4, NW = kPwWaves;  // k-steps of token operands in flight
+    constexpr int kLds = pw_lds_per_wave(NT);
     extern __shared__ __align__(16) unsigned char lds[];
     const int lane = threadIdx.x & 63, wave = wave_id();
-    float4* lv = reinterpret_cast<float4*>(lds + (size_t)wave * kPwLdsPerWave);  // [level 2..3][tile][q][lane]
-    float* dd = reinterpret_cast<float*>(lds + (size_t)wave * kPwLdsPerWave + 2 * kPwLevelBytes);  // d[32], dmin[32]
+    float4* lv = reinterpret_cast<float4*>(lds + (size_t)wave * kLds);  // [level 2..][tile][q][lane]
+    float* dd = reinterpret_cast<float*>(lds + (size_t)wave * kLds + 2 * pw_level_bytes(NT));  // d[32], dmin[32]
 
     // Workgroup i runs on XCD i % 8: the TP token groups of one 128-row group
     // get consecutive slots of one XCD, so its weights stream into one L2.
@@ -605,13 +613,31 @@ static void launch_gemm_lv(dim3 grid, hipStream_t stream, const uint8_t* w, Gemm
     hipLaunchKernelGGL(q4k_gemm_kernel<LV>, grid, dim3(256), 0, stream, w, ws, y, R, N, M, NR, TT);
 }
 
-static hipError_t launch_pw(hipStream_t stream, const uint8_t* w, GemmWs ws, float* y, int R, int N, int M, int Mt) {
-    const int NG = (N + 32 * kPwWaves - 1) / (32 * kPwWaves), TP = (Mt + 1) / 2;
-    const size_t lds = (size_t)kPwWaves * kPwLdsPerWave;
-    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(&q4k_gemm_pw_kernel), lds)) return e;
-    hipLaunchKernelGGL(q4k_gemm_pw_kernel, dim3((unsigned)NG * (unsigned)TP), dim3(kPwWaves * 64), lds, stream, w, ws,
-                       y, R, N, M, NG, TP);
+template <int NT>
+static hipError_t launch_pw_t(hipStream_t stream, const uint8_t* w, GemmWs ws, float* y, int R, int N, int M, int NG,
+                              int TP) {
+    const size_t lds = (size_t)kPwWaves * pw_lds_per_wave(NT);
+    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(&q4k_gemm_pw_kernel<NT>), lds)) return e;
+    hipLaunchKernelGGL((q4k_gemm_pw_kernel<NT>), dim3((unsigned)NG * (unsigned)TP), dim3(kPwWaves * 64), lds,
+                       stream, w, ws, y, R, N, M, NG, TP);
     return hipGetLastError();
+}
+
+// Which per-wave form takes a launch: 0 none (the LDS-operand kernel), else
+// the token tiles per wave: two, unless that leaves fewer than 512
+// workgroups (two per CU) and one tile per wave makes more.  The buffer
+// descriptors address the weights with 32-bit offsets.
+static int pw_tiles(int R, int N, int Mt) {
+    if (R > kPwMaxR || (size_t)N * R * 144 >= ((size_t)1 << 31)) return 0;
+    const int NG = (N + 32 * kPwWaves - 1) / (32 * kPwWaves);
+    return (NG * ((Mt + 1) / 2) < 512 && Mt > 1) ? 1 : 2;
+}
+
+static hipError_t launch_pw(hipStream_t stream, const uint8_t* w, GemmWs ws, float* y, int R, int N, int M, int Mt,
+                            int nt) {
+    const int NG = (N + 32 * kPwWaves - 1) / (32 * kPwWaves);
+    const int TP = nt == 1 ? Mt : (Mt + 1) / 2;
+    return nt == 1 ? launch_pw_t<1>(stream, w, ws, y, R, N, M, NG, TP) : launch_pw_t<2>(stream, w, ws, y, R, N, M, NG, TP);
 }
 
 hipError_t launch_q4k_gemm(const float* x, const uint8_t* w, float* y, int batch, int in_feat, int out_feat,
@@ -624,16 +650,16 @@ hipError_t launch_q4k_gemm(const float* x, const uint8_t* w, float* y, int batch
     for (int b0 = 0; b0 < batch; b0 += kChunkM) {
         const int M = min(batch - b0, kChunkM), Mp = (M + 31) / 32 * 32;
         const GemmWs ws = gemm_ws(workspace, Mp, R);
-        // rows of at most 16 super-blocks take the per-wave kernel (its buffer
-        // descriptors address the weights with 32-bit offsets); Mp is a
-        // multiple of 32, so Mp / 16 pre-pass groups cover every token slot
-        const bool pw = R <= kPwMaxR && (size_t)out_feat * R * 144 < ((size_t)1 << 31);
+        // the per-wave kernel where pw_tiles allows it; Mp is a multiple of
+        // 32, so Mp / 16 pre-pass groups cover every token slot
+        const int nt = pw_tiles(R, out_feat, Mp / 32);
+        const bool pw = nt > 0;
         hipLaunchKernelGGL(act_quant_tiles_kernel, dim3((unsigned)R, (unsigned)(Mp / kQuantWaves)),
                            dim3(kQuantWaves * 64), 0, stream, x + (size_t)b0 * in_feat, ws, R, M, pw ? 1 : 0);
         if (hipError_t e = hipGetLastError()) return e;
         float* yb = y + (size_t)b0 * out_feat;
         if (pw) {
-            if (hipError_t e = launch_pw(stream, w, ws, yb, R, out_feat, M, Mp / 32)) return e;
+            if (hipError_t e = launch_pw(stream, w, ws, yb, R, out_feat, M, Mp / 32, nt)) return e;
             continue;
         }
         const int TT = (M + kTB - 1) / kTB;
