@@ -92,6 +92,8 @@ def test_runtime_library_exports_its_header():
     lib = runtime.lib()
     assert lib.vtqrt_run(None, 0, b"m", None, None, 1, 1, None, None, None, None) == vtq.E_INVALID_ARGUMENT
     assert b"null" in lib.vtqrt_last_error(None)
+    # the prompt mode needs a model and one of the two documented values
+    assert lib.vtqrt_set_prompt_mode(None, runtime.PROMPT_BATCHED) == vtq.E_INVALID_ARGUMENT
 
 
 def test_runtime_blake3_matches_oracle_on_cpu():

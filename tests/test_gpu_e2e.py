@@ -147,6 +147,15 @@ def test_e2e_errors_mirror_reference():
             gm.close()
     with pytest.raises(Exception, match="bad magic"):
         runtime.Model(np.frombuffer(b"GGML" + b"\0" * 60, dtype=np.uint8))
+    gm = runtime.Model(blob)
+    try:
+        import vtq
+
+        for bad in (-1, 2):
+            assert runtime.lib().vtqrt_set_prompt_mode(gm.handle, bad) == vtq.E_INVALID_ARGUMENT
+        gm.run(prompt, 2, b"\0" * 32)  # the mode in force is unchanged
+    finally:
+        gm.close()
 
 
 def test_e2e_config5_full_bit_exact():
