@@ -95,7 +95,7 @@ def test_q6k_integer_synthetic(ctx, batch, in_f, out_f):
     check(ctx, vtq.Q6_K, 0, x, w, batch, in_f, out_f)
 
 
-# batch >= 32 takes the i8-MFMA prefill GEMM (token tiles of 128, row tiles of 32)
+# batch >= 32 takes the i8-MFMA prefill GEMM (split-K at these grid sizes)
 GEMM_SHAPES = [(32, 256, 32), (33, 512, 1), (64, 4096, 100), (130, 2048, 70), (128, 5632, 64),
                (256, 11008, 40), (40, 256 * 127, 8), (300, 4096, 33)]
 
@@ -107,17 +107,44 @@ def test_q4k_prefill_gemm(ctx, batch, in_f, out_f):
     check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
 
 
-# rows of at most 16 super-blocks take the per-wave GEMM (32 rows per wave,
-# 128-row workgroups; one 32-token tile per wave at these grid sizes): every
-# row length 1..16 (each tree shape of its counter), token counts either side
-# of the 32- and 64-token tiles, row counts either side of the 32-row tiles
-# and the 128-row workgroups
-PW_SHAPES = [(32, 256, 129), (64, 512, 1), (33, 768, 129), (65, 1024, 300), (96, 1280, 128), (97, 1536, 513),
+# small grids take the split-K GEMM (one 32-row x 32-token tile per
+# workgroup, the row's super-blocks cut into fixed_tree subtrees): every row
+# length 1..16 (each tree shape of its counter), token counts either side of
+# the 32-token tiles, row counts either side of the 32-row tiles
+SHORT_ROW_SHAPES = [(32, 256, 129), (64, 512, 1), (33, 768, 129), (65, 1024, 300), (96, 1280, 128), (97, 1536, 513),
              (127, 1792, 31), (128, 2048, 130), (34, 2304, 64), (200, 2560, 257), (70, 2816, 77),
              (160, 3072, 96), (129, 3328, 33), (95, 3584, 200), (63, 3840, 127), (192, 4096, 255)]
-# grids of at least 512 workgroups take two 32-token tiles per wave: an odd
-# tile count (the last wave's second tile repeats the last one) and ragged rows
-PW2_SHAPES = [(272, 768, 13312), (300, 256, 13313), (512, 1024, 13000)]
+# rows of at most 16 super-blocks over more than 1024 tiles take the per-wave
+# GEMM with two 32-token tiles per wave: an odd tile count (the last wave's
+# second tile repeats the last one), ragged rows, row lengths 1, 3, 4, 11, 16
+PW2_SHAPES = [(272, 768, 13312), (300, 256, 13313), (512, 1024, 13000), (257, 16 * 256, 4200),
+              (200, 11 * 256, 6000)]
+# rows longer than 16 super-blocks where the LDS-operand GEMM launches at
+# least 256 workgroups (one per 32 rows x 128 tokens)
+LDS_SHAPES = [(129, 17 * 256, 4096), (130, 33 * 256, 4096), (257, 20 * 256, 3000), (160, 70 * 256, 8192)]
+
+
+# split-K rows longer than 16 super-blocks: each piece size C = 1, 2, 4, 8,
+# 16, trees smaller than a piece (R = 17, 33, 65, 97), a row length of one
+# whole tree (R = 64), the prompt pass's W2 shape (R = 22, 2048 rows, 128
+# tokens)
+SK_SHAPES = [(37, 12 * 256, 70), (33, 22 * 256, 2048), (32, 40 * 256, 100), (64, 100 * 256, 33),
+             (40, 127 * 256, 40), (95, 17 * 256, 96), (34, 33 * 256, 130), (65, 65 * 256, 64),
+             (41, 97 * 256, 31), (100, 64 * 256, 64), (128, 22 * 256, 2048), (130, 43 * 256, 1000)]
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", SK_SHAPES)
+def test_q4k_prefill_gemm_split_k_shapes(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 7 + out_f)
+    x = synth.activations(batch * in_f, seed=in_f * 23 + batch)
+    check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
+
+
+@pytest.mark.parametrize("batch,in_f,out_f", LDS_SHAPES)
+def test_q4k_prefill_gemm_lds_operand_shapes(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 3 + out_f)
+    x = synth.activations(batch * in_f, seed=in_f * 29 + batch)
+    check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
 
 
 @pytest.mark.parametrize("batch,in_f,out_f", PW2_SHAPES)
@@ -127,8 +154,8 @@ def test_q4k_prefill_gemm_two_tiles_per_wave(ctx, batch, in_f, out_f):
     check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
 
 
-@pytest.mark.parametrize("batch,in_f,out_f", PW_SHAPES)
-def test_q4k_prefill_gemm_per_wave_shapes(ctx, batch, in_f, out_f):
+@pytest.mark.parametrize("batch,in_f,out_f", SHORT_ROW_SHAPES)
+def test_q4k_prefill_gemm_short_row_lengths(ctx, batch, in_f, out_f):
     w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 13 + out_f)
     x = synth.activations(batch * in_f, seed=in_f * 17 + batch)
     check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)

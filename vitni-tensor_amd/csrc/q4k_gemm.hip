@@ -20,10 +20,13 @@
 // fixed_tree(p[0..R)) == fold-right over the balanced trees of the binary
 // digits of R, each built left to right as parts arrive.
 //
-// Two kernels share the activation pre-pass, which writes the token codes in
-// the MFMA operand order:
+// Three kernels share the activation pre-pass, which writes the token codes
+// in the MFMA operand order (gemm_form picks one per launch):
 //  * q4k_gemm_pw_kernel (rows of at most 16 super-blocks): each wave forms
 //    its own weight operands in registers, no barriers;
+//  * q4k_gemm_sk_kernel (grids too small to fill the chip): the same
+//    per-wave fold over whole fixed_tree subtrees of a row, one per wave of
+//    a workgroup, combined in the tree's order;
 //  * q4k_gemm_kernel (longer rows): a workgroup of 4 waves owns 32 weight
 //    rows x 128 tokens and builds the weight operands once per super-block
 //    in LDS.
@@ -373,30 +376,16 @@ __device__ __forceinline__ uint32_t pk_f16(uint32_t a, uint32_t b) {  // two sma
     return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz((float)a, (float)b));
 }
 
+// The per-wave work: rows o0 .. o0+31 and token tiles NT*tp .. NT*tp+NT-1,
+// the parts of super-blocks s0 .. s0+Rl-1 folded by fixed_tree over those Rl
+// leaves into res (the row's result when s0 = 0 and Rl = R; the value of one
+// subtree when Rl is a power of two and s0 a multiple of it).  Rl <= 16.
+// lv: this wave's LDS tree levels 2 and 3; dd: its d / dmin slots.
 template <int NT>
-__global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uint8_t* __restrict__ W, GemmWs ws,
-                                                                       float* __restrict__ y, int R, int N, int M,
-                                                                       int NG, int TP) {
-    constexpr int D = 4, NW = kPwWaves;  // k-steps of token operands in flight
-    constexpr int kLds = pw_lds_per_wave(NT);
-    extern __shared__ __align__(16) unsigned char lds[];
-    const int lane = threadIdx.x & 63, wave = wave_id();
-    float4* lv = reinterpret_cast<float4*>(lds + (size_t)wave * kLds);  // [level 2..][tile][q][lane]
-    float* dd = reinterpret_cast<float*>(lds + (size_t)wave * kLds + 2 * pw_level_bytes(NT));  // d[32], dmin[32]
-
-    // Workgroup i runs on XCD i % 8: the TP token groups of one 128-row group
-    // get consecutive slots of one XCD, so its weights stream into one L2.
-    const int id = blockIdx.x, full = (NG / 8) * 8 * TP;
-    int rg, tp;
-    if (id < full) {
-        const int k = id >> 3;
-        rg = (k / TP) * 8 + (id & 7);
-        tp = k % TP;
-    } else {
-        rg = (NG / 8) * 8 + (id - full) / TP;
-        tp = (id - full) % TP;
-    }
-    const int o0 = (rg * NW + wave) * 32;
+__device__ __forceinline__ void pw_tree(const uint8_t* __restrict__ W, const GemmWs& ws, int R, int N, int M, int o0,
+                                        int tp, int s0, int Rl, float4* lv, float* dd, float (&res)[NT][16]) {
+    constexpr int D = 4;  // k-steps of token operands in flight
+    const int lane = threadIdx.x & 63;
     const int r = lane & 31, g = lane >> 5;
     const int Mt = (M + 31) / 32;
 
@@ -409,15 +398,15 @@ __global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uin
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const uint32_t T = (uint32_t)min(NT * tp + t, Mt - 1);
-        q0[t] = T * R * 8192;
-        m0[t] = T * R * 1024;
-        d0[t] = T * R * 128;
+        q0[t] = (T * R + s0) * 8192;
+        m0[t] = (T * R + s0) * 1024;
+        d0[t] = (T * R + s0) * 128;
     }
     const uint32_t vq = 16u * lane, vd = 4u * r;
     // lane (r, g): header of row r, and code bytes 32h + 16g .. +15 of each
     // quarter h: low nibbles are k-step 2h, high nibbles k-step 2h + 1, both
     // at k = 16g .. 16g + 15 of the step (the B operand's order)
-    const uint32_t vh = (uint32_t)min(o0 + r, N - 1) * ((uint32_t)R * 144), vc = vh + 16 + 16 * g;
+    const uint32_t vh = (uint32_t)min(o0 + r, N - 1) * ((uint32_t)R * 144) + (uint32_t)s0 * 144, vc = vh + 16 + 16 * g;
 
     uint4 hdr = __builtin_bit_cast(uint4, bload16(rw, vh, 0));
     uint4 qw[4];
@@ -440,7 +429,7 @@ __global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uin
 
     // one super-block: the parts of every tile into p
     auto sblock = [&](int s, float (&p)[NT][16]) __attribute__((always_inline)) {
-        const int sn = min(s + 1, R - 1);
+        const int sn = min(s + 1, Rl - 1);
         // get_scale_min_k4 (src/ops/quant.rs:267-276) of all eight sub-blocks, a byte each
         const uint32_t Y = hdr.y, Z = hdr.z, Wd = hdr.w;
         const uint32_t SCl = Y & 0x3F3F3F3Fu, Ml = Z & 0x3F3F3F3Fu;
@@ -542,7 +531,7 @@ __global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uin
     // fixed_tree (src/ops/quant.rs:461-476) as a binary counter over s: after
     // leaf s the levels below L = (trailing ones of s) merge into level L.
     int s = 0;
-    for (; s + 1 < R; s++) {
+    for (; s + 1 < Rl; s++) {
         float p[NT][16];
         sblock(s, p);
         const int L = __builtin_ctz(~s);
@@ -563,7 +552,6 @@ __global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uin
             }
         }
     }
-    float res[NT][16];
     {
         // last leaf: merge the levels below L, then fold the blocks still open
         // (the set bits of R above L) right to left
@@ -573,10 +561,40 @@ __global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uin
         if (L >= 2) reg_merge(L1, res);
         if (L >= 3) lds_merge(2, res);
         if (L >= 4) lds_merge(3, res);
-        if (L < 1 && ((R >> 1) & 1)) reg_merge(L1, res);
-        if (L < 2 && ((R >> 2) & 1)) lds_merge(2, res);
-        if (L < 3 && ((R >> 3) & 1)) lds_merge(3, res);
+        if (L < 1 && ((Rl >> 1) & 1)) reg_merge(L1, res);
+        if (L < 2 && ((Rl >> 2) & 1)) lds_merge(2, res);
+        if (L < 3 && ((Rl >> 3) & 1)) lds_merge(3, res);
     }
+}
+
+template <int NT>
+__global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uint8_t* __restrict__ W, GemmWs ws,
+                                                                       float* __restrict__ y, int R, int N, int M,
+                                                                       int NG, int TP) {
+    constexpr int NW = kPwWaves;
+    constexpr int kLds = pw_lds_per_wave(NT);
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    float4* lv = reinterpret_cast<float4*>(lds + (size_t)wave * kLds);  // [level 2..][tile][q][lane]
+    float* dd = reinterpret_cast<float*>(lds + (size_t)wave * kLds + 2 * pw_level_bytes(NT));  // d[32], dmin[32]
+
+    // Workgroup i runs on XCD i % 8: the TP token groups of one 128-row group
+    // get consecutive slots of one XCD, so its weights stream into one L2.
+    const int id = blockIdx.x, full = (NG / 8) * 8 * TP;
+    int rg, tp;
+    if (id < full) {
+        const int k = id >> 3;
+        rg = (k / TP) * 8 + (id & 7);
+        tp = k % TP;
+    } else {
+        rg = (NG / 8) * 8 + (id - full) / TP;
+        tp = (id - full) % TP;
+    }
+    const int o0 = (rg * NW + wave) * 32;
+    const int r = lane & 31, g = lane >> 5;
+    const int Mt = (M + 31) / 32;
+    float res[NT][16];
+    pw_tree<NT>(W, ws, R, N, M, o0, tp, 0, R, lv, dd, res);
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         const int T = NT * tp + t, tok = T * 32 + r;
@@ -594,6 +612,118 @@ __global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uin
                     for (int e = 0; e < 4; e++)
                         if (o + e < N) yrow[o + e] = res[t][4 * q + e];
                 }
+            }
+        }
+    }
+}
+
+// Split-K for grids too small to fill the chip (prompt-sized batches): a
+// workgroup owns one 32-row tile and one 32-token tile, and wave w folds
+// chunk w of the row's super-blocks with pw_tree.  The chunks are whole
+// subtrees of fixed_tree: the balanced trees of R's binary digits (from the
+// highest), each cut into pieces of C leaves (a tree smaller than C is one
+// piece).  Wave 0 then combines the chunk values as fixed_tree does: within
+// each tree pairwise, level by level, and the trees folded right to left
+// (fixed_tree(p[0..R)) == T_high + (... + T_low)).  Any row length to 127
+// super-blocks: C <= 16 keeps pw_tree's counter within its four levels.
+constexpr int kSkMaxWaves = 12;
+
+__host__ __device__ inline int sk_chunks(int R, int C) {
+    int n = 0;
+    for (int k = 6; k >= 0; k--)
+        if ((R >> k) & 1) n += (1 << k) >= C ? (1 << k) / C : 1;
+    return n;
+}
+
+// The piece size for a grid of T tiles: the smallest that keeps the launch
+// within 2048 waves (8 per CU), else the smallest that needs at most
+// kSkMaxWaves chunks (every row length below 128 super-blocks has one).
+static int sk_piece(int R, int T) {
+    int first = 0;
+    for (int C = 1; C <= 16; C <<= 1) {
+        const int n = sk_chunks(R, C);
+        if (n > kSkMaxWaves) continue;
+        if (!first) first = C;
+        if ((long)T * n <= 2048) return C;
+    }
+    return first;
+}
+
+__global__ __launch_bounds__(kSkMaxWaves * 64, 1) void q4k_gemm_sk_kernel(const uint8_t* __restrict__ W, GemmWs ws,
+                                                                           float* __restrict__ y, int R, int N, int M,
+                                                                           int C) {
+    constexpr int kW = pw_lds_per_wave(1);
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int lane = threadIdx.x & 63, wave = wave_id(), nw = (int)(blockDim.x >> 6);
+    float4* lv = reinterpret_cast<float4*>(lds + (size_t)wave * kW);
+    float* dd = reinterpret_cast<float*>(lds + (size_t)wave * kW + 2 * pw_level_bytes(1));
+    float4* cv = reinterpret_cast<float4*>(lds + (size_t)nw * kW);  // [chunk][q][lane]
+    const int Mt = (M + 31) / 32, rt = (int)blockIdx.x / Mt, tt = (int)blockIdx.x % Mt;
+    const int r = lane & 31, g = lane >> 5;
+    // this wave's chunk
+    int s0 = 0, len = 0;
+    {
+        int i = wave, base = 0;
+        for (int k = 6; k >= 0; k--) {
+            if (!((R >> k) & 1)) continue;
+            const int size = 1 << k, n = size >= C ? size / C : 1, sz = size >= C ? C : size;
+            if (i < n) {
+                s0 = base + i * sz;
+                len = sz;
+                break;
+            }
+            i -= n;
+            base += size;
+        }
+    }
+    float res[1][16];
+    pw_tree<1>(W, ws, R, N, M, rt * 32, tt, s0, len, lv, dd, res);
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+        cv[(wave * 4 + q) * 64 + lane] = make_float4(res[0][4 * q], res[0][4 * q + 1], res[0][4 * q + 2], res[0][4 * q + 3]);
+    __syncthreads();
+    if (wave != 0) return;
+    // the trees from the lowest binary digit up (the fold runs right to
+    // left); a tree's first chunk follows the chunks of the digits above it
+    auto pieces = [&](int k) { return (1 << k) >= C ? (1 << k) / C : 1; };
+    float acc[16];
+    bool first = true;
+    for (int k = 0; k < 7; k++) {
+        if (!((R >> k) & 1)) continue;
+        int c0 = 0;
+        for (int k2 = k + 1; k2 < 7; k2++)
+            if ((R >> k2) & 1) c0 += pieces(k2);
+        const int n = pieces(k);
+        for (int st = 1; st < n; st <<= 1)
+            for (int i = 0; i + st < n; i += 2 * st)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float4& a = cv[((c0 + i) * 4 + q) * 64 + lane];
+                    const float4 b = cv[((c0 + i + st) * 4 + q) * 64 + lane];
+                    a = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+                }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 tv = cv[(c0 * 4 + q) * 64 + lane];
+            const float t4[4] = {tv.x, tv.y, tv.z, tv.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[4 * q + e] = first ? t4[e] : t4[e] + acc[4 * q + e];
+        }
+        first = false;
+    }
+    const int tok = tt * 32 + r;
+    if (tok < M) {
+        float* yrow = y + (size_t)tok * N;
+        const bool vec = (N & 3) == 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int o = rt * 32 + 8 * q + 4 * g;
+            if (vec && o + 3 < N) {
+                *reinterpret_cast<float4*>(yrow + o) = make_float4(acc[4 * q], acc[4 * q + 1], acc[4 * q + 2], acc[4 * q + 3]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (o + e < N) yrow[o + e] = acc[4 * q + e];
             }
         }
     }
@@ -623,21 +753,37 @@ static hipError_t launch_pw_t(hipStream_t stream, const uint8_t* w, GemmWs ws, f
     return hipGetLastError();
 }
 
-// Which per-wave form takes a launch: 0 none (the LDS-operand kernel), else
-// the token tiles per wave: two, unless that leaves fewer than 512
-// workgroups (two per CU) and one tile per wave makes more.  The buffer
-// descriptors address the weights with 32-bit offsets.
-static int pw_tiles(int R, int N, int Mt) {
-    if (R > kPwMaxR || (size_t)N * R * 144 >= ((size_t)1 << 31)) return 0;
-    const int NG = (N + 32 * kPwWaves - 1) / (32 * kPwWaves);
-    return (NG * ((Mt + 1) / 2) < 512 && Mt > 1) ? 1 : 2;
+// Which kernel takes a launch (M tokens in Mt 32-token tiles): 3 the
+// split-K kernel, for grids too small to fill the chip; else 2 the per-wave
+// kernel with two token tiles per wave for rows of at most 16 super-blocks,
+// 0 the LDS-operand kernel for longer rows.  Split-K takes rows of at most 16
+// super-blocks up to 1024 tiles of 32 x 32, and longer rows where the
+// LDS-operand kernel would launch fewer than 256 workgroups (measured
+// crossovers, pre-pass included: 4096 x 4096 at 256 tokens 25.5 against
+// 26.3 us for the LDS-operand kernel, 11264 x 2048 at 96 tokens 19.5 against
+// 18.8 us for the per-wave kernel; 4096 x 11008 at 128 tokens 43.4 against
+// 56.5 us, at 256 tokens 76.6 against 59.3 us).  The split-K and per-wave
+// forms address the weights with 32-bit buffer offsets.
+static int gemm_form(int R, int N, int M, int Mt) {
+    if ((size_t)N * R * 144 >= ((size_t)1 << 31)) return 0;
+    if (R <= kPwMaxR) return (long)((N + 31) / 32) * Mt <= 1024 ? 3 : 2;
+    return (long)((N + kTO - 1) / kTO) * ((M + kTB - 1) / kTB) < 256 ? 3 : 0;
 }
 
-static hipError_t launch_pw(hipStream_t stream, const uint8_t* w, GemmWs ws, float* y, int R, int N, int M, int Mt,
-                            int nt) {
+static hipError_t launch_sk(hipStream_t stream, const uint8_t* w, GemmWs ws, float* y, int R, int N, int M, int Mt) {
+    const unsigned NR = (unsigned)((N + 31) / 32);
+    const int C = sk_piece(R, (int)NR * Mt), nw = sk_chunks(R, C);
+    if (C == 0 || nw > kSkMaxWaves) return hipErrorInvalidValue;
+    const size_t lds = (size_t)nw * pw_lds_per_wave(1) + (size_t)nw * 4 * 64 * 16;
+    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(&q4k_gemm_sk_kernel), lds)) return e;
+    hipLaunchKernelGGL(q4k_gemm_sk_kernel, dim3(NR * (unsigned)Mt), dim3((unsigned)nw * 64), lds, stream, w, ws, y, R,
+                       N, M, C);
+    return hipGetLastError();
+}
+
+static hipError_t launch_pw(hipStream_t stream, const uint8_t* w, GemmWs ws, float* y, int R, int N, int M, int Mt) {
     const int NG = (N + 32 * kPwWaves - 1) / (32 * kPwWaves);
-    const int TP = nt == 1 ? Mt : (Mt + 1) / 2;
-    return nt == 1 ? launch_pw_t<1>(stream, w, ws, y, R, N, M, NG, TP) : launch_pw_t<2>(stream, w, ws, y, R, N, M, NG, TP);
+    return launch_pw_t<2>(stream, w, ws, y, R, N, M, NG, (Mt + 1) / 2);
 }
 
 hipError_t launch_q4k_gemm(const float* x, const uint8_t* w, float* y, int batch, int in_feat, int out_feat,
@@ -650,16 +796,19 @@ hipError_t launch_q4k_gemm(const float* x, const uint8_t* w, float* y, int batch
     for (int b0 = 0; b0 < batch; b0 += kChunkM) {
         const int M = min(batch - b0, kChunkM), Mp = (M + 31) / 32 * 32;
         const GemmWs ws = gemm_ws(workspace, Mp, R);
-        // the per-wave kernel where pw_tiles allows it; Mp is a multiple of
-        // 32, so Mp / 16 pre-pass groups cover every token slot
-        const int nt = pw_tiles(R, out_feat, Mp / 32);
-        const bool pw = nt > 0;
+        // the per-wave forms where gemm_form allows them (both read the
+        // f16 min-term operand); Mp is a multiple of 32, so Mp / 16 pre-pass
+        // groups cover every token slot
+        const int form = gemm_form(R, out_feat, M, Mp / 32);
+        const bool pw = form != 0;
         hipLaunchKernelGGL(act_quant_tiles_kernel, dim3((unsigned)R, (unsigned)(Mp / kQuantWaves)),
                            dim3(kQuantWaves * 64), 0, stream, x + (size_t)b0 * in_feat, ws, R, M, pw ? 1 : 0);
         if (hipError_t e = hipGetLastError()) return e;
         float* yb = y + (size_t)b0 * out_feat;
         if (pw) {
-            if (hipError_t e = launch_pw(stream, w, ws, yb, R, out_feat, M, Mp / 32, nt)) return e;
+            const hipError_t e = form == 3 ? launch_sk(stream, w, ws, yb, R, out_feat, M, Mp / 32)
+                                           : launch_pw(stream, w, ws, yb, R, out_feat, M, Mp / 32);
+            if (e) return e;
             continue;
         }
         const int TT = (M + kTB - 1) / kTB;
