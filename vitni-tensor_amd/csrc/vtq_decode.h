@@ -40,11 +40,17 @@ hipError_t rms_norm_rows(const float* x, const float* w, int n, int rows, float 
 // Byte ranges later kernels of the step read, streamed through the
 // memory-side cache by `groups` extra workgroups of the attention launch
 // (which leaves most CUs idle), so that those kernels read them from the
-// cache.  The loaded bytes are folded into one value, stored to sink only if
+// cache.  A range of cached k or v rows gives its row size: only the rows
+// before the step's position (*pos) are streamed.  The loaded bytes are folded into one value, stored to sink only if
 // it equals magic, so the loads are kept and nothing is written in practice.
 struct Prefetch {
-    const uint8_t* p[4] = {nullptr, nullptr, nullptr, nullptr};
-    uint32_t n[4] = {0, 0, 0, 0};
+    static constexpr int kRanges = 6;
+    const uint8_t* p[kRanges] = {};
+    uint32_t n[kRanges] = {};
+    // nonzero: the range holds cached rows, and only rows 0 .. *pos - 1 of
+    // row_bytes each (at most n) are streamed
+    uint32_t row_bytes[kRanges] = {};
+    const int* pos = nullptr;
     int groups = 0;
     uint32_t magic = 0;
     uint32_t* sink = nullptr;

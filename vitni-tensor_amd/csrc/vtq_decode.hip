@@ -192,12 +192,14 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 __device__ void prefetch_ranges(const Prefetch& pf, int g, int G) {
     uint32_t acc = 0;
     const uint32_t step = (uint32_t)G * blockDim.x * 16u;
+    const uint32_t rows = pf.pos ? (uint32_t)max(*pf.pos, 0) : 0u;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        if (!pf.n[r]) continue;
+    for (int r = 0; r < Prefetch::kRanges; r++) {
+        const uint32_t n = pf.row_bytes[r] ? min(pf.n[r], rows * pf.row_bytes[r]) : pf.n[r];
+        if (!n) continue;
         const __amdgpu_buffer_rsrc_t rs =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(pf.p[r]), (short)0, (int)pf.n[r], 0x00020000);
-        for (uint32_t off = ((uint32_t)g * blockDim.x + threadIdx.x) * 16u; off < pf.n[r]; off += 4 * step) {
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(pf.p[r]), (short)0, (int)n, 0x00020000);
+        for (uint32_t off = ((uint32_t)g * blockDim.x + threadIdx.x) * 16u; off < n; off += 4 * step) {
             uint32_t o[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) o[u] = off + (uint32_t)u * step;  // out of range: zeros, no traffic

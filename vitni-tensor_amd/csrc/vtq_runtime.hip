@@ -294,19 +294,18 @@ vtq::decode::EmbedArgs embed_args(vtqrt_model* m) {
                                   vtq::decode::embed_row_bytes(m->tok.type, m->dim), m->dim, m->x, rope_args(m)};
 }
 
-// a range for the attention launch's prefetch workgroups (at most four)
-void pf_add(vtq::decode::Prefetch& pf, const uint8_t* p, size_t n) {
-    for (int r = 0; r < 4; r++)
+// a range for the attention launch's prefetch workgroups; row_bytes nonzero:
+// cached rows, of which only 0 .. *pos - 1 are read
+void pf_add(vtq::decode::Prefetch& pf, const uint8_t* p, size_t n, uint32_t row_bytes = 0) {
+    for (int r = 0; r < vtq::decode::Prefetch::kRanges; r++)
         if (!pf.n[r]) {
             pf.p[r] = p;
             pf.n[r] = (uint32_t)std::min<size_t>(n, (size_t)1 << 31);
+            pf.row_bytes[r] = row_bytes;
             return;
         }
 }
 
-// One decode step at position *m->pos (forward_quantized::step), enqueued
-// on m->stream.  x holds the step's embedding row on entry (the previous
-// step's argmax kernel, or the run's first embedding, wrote it).
 int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* hist) {
     namespace dec = vtq::decode;
     const int dim = m->dim, head = dim / m->heads, kv_dim = m->kv_heads * head, hidden = m->hidden;
@@ -344,9 +343,10 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
         a.att_g = m->att_g;
         {
             // The attention launch uses one workgroup per head and leaves the
-            // other CUs idle: one extra workgroup on each streams the weights
-            // the layer reads next (Wo, W1 | W3, the next layer's q | k | v)
-            // through the memory-side cache, so those GEMVs find them there.
+            // other CUs idle: one extra workgroup on each streams what the
+            // step reads next (Wo, W1 | W3, the next layer's q | k | v and its
+            // cached k and v rows) through the memory-side cache, so the
+            // kernels that follow find it there.
             dec::Prefetch& pf = a.pf;
             pf.magic = 0xA5A5A5A5u;
             pf.sink = m->pf_sink;
@@ -363,6 +363,12 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
                     pf_add(pf, m->dblob + Ln.wq.dev, Ln.wq.nbytes + Ln.wk.nbytes + Ln.wv.nbytes);
                 else
                     pf_add(pf, m->dblob + Ln.wq.dev, Ln.wq.nbytes);
+                // and the next layer's cached k and v rows 0 .. pos-1, which
+                // its attention reads (the row count is read on the device)
+                const size_t lay = (size_t)m->seq * kv_dim * 4;
+                pf.pos = m->pos;
+                pf_add(pf, reinterpret_cast<const uint8_t*>(m->kc) + (size_t)(l + 1) * lay, lay, (uint32_t)kv_dim * 4);
+                pf_add(pf, reinterpret_cast<const uint8_t*>(m->vc) + (size_t)(l + 1) * lay, lay, (uint32_t)kv_dim * 4);
             }
             pf.groups = std::max(0, m->num_cus - m->heads);
         }
