@@ -13,7 +13,8 @@
 //    v_mfma_i32_32x32x32_i8 whose accumulators run over all 256 elements;
 //  * the min term pairs m_j with bsum_j = 64*bh_j + bl_j: two i8 MFMAs and
 //    accm = 64*Ch + Cl in the LDS-operand kernel, one f16 MFMA in the
-//    per-wave kernel (see there why that is exact).
+//    per-wave and split-K kernels (see the per-wave kernel for why that is
+//    exact).
 // Integer sums are exact in any order, so the MFMA reduction order is free.
 // The float epilogue is the reference's, per (b, o, s), in VALU, and the
 // fixed_tree over super-blocks is a streamed binary counter:
@@ -353,8 +354,8 @@ __global__ __launch_bounds__(256, 2) void q4k_gemm_kernel(const uint8_t* __restr
 // the last super-block the counter folds straight into the result, so level
 // 4 (R = 16) is never stored.
 //
-// Template parameter NT: token tiles per wave (2; 1 where two would leave
-// fewer than two workgroups per CU, as at prompt-sized batches).
+// Template parameter NT: token tiles per wave (2 in q4k_gemm_pw_kernel; the
+// split-K kernel folds one tile per wave with pw_tree<1>).
 constexpr int kPwWaves = 4;
 constexpr int kPwMaxR = 16;
 __host__ __device__ constexpr int pw_level_bytes(int NT) { return NT * 4 * 64 * 16; }  // one tree level of NT tiles
