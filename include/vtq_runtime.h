@@ -102,8 +102,9 @@ int vtqrt_run(vtqrt_model *m, int regime, const char *model_id, const uint8_t we
 /* How vtqrt_run processes the prompt.  VTQRT_PROMPT_BATCHED (the default):
  * positions 0 .. prompt_len-1 in one pass, every linear over all prompt
  * rows at once (the prefill GEMM for Q4_K), then the decode steps from
- * position prompt_len; where a position's scores do not fit in LDS, or with
- * a one-token prompt, it steps as below.  VTQRT_PROMPT_STEPWISE: one
+ * position prompt_len; where the pass's attention does not fit in LDS (a
+ * position's scores and one tile of cached rows: prompts beyond about 39,800
+ * positions at head_dim 64), or with a one-token prompt, it steps as below.  VTQRT_PROMPT_STEPWISE: one
  * forward_quantized::step per position, as run_quantized's loop
  * (src/model/inference.rs:313-329).  Both give the same tokens, digests and
  * logits bit for bit: the reference's batch rows are independent, and each

@@ -71,7 +71,7 @@ struct AttnArgs {
     float* att_g = nullptr;
     // 0: one decode step at *pos.  P > 0: a prompt pass over positions
     // 0..P-1 at once (qkv, cs and out hold P rows; rope_cache_rows has
-    // written every position's k and v; the scores must fit in LDS)
+    // written every position's k and v; see attention_rows_supported)
     int batched = 0;
     Prefetch pf;  // extra workgroups (one-step launches only)
 };
@@ -84,6 +84,10 @@ struct AttnArgs {
 bool attention_supported(int head_dim, int seq);
 bool attention_scores_in_lds(int head_dim, int seq);
 hipError_t attention(const AttnArgs& a, hipStream_t stream);
+// Whether a prompt pass of P positions can run its attention: one wave per
+// (query head, position), the waves of a workgroup on one KV group, each
+// wave's q and P scores and one tile of cached rows in LDS.
+bool attention_rows_supported(int head_dim, int P, int heads, int kv_heads);
 // The prompt pass's cache write: position p's k (bias, RoPE) and v for
 // p < a.batched, as attention computes them for its own position.
 hipError_t rope_cache_rows(const AttnArgs& a, hipStream_t stream);

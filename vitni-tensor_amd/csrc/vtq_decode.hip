@@ -254,8 +254,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float* vp = kp + hd;
     float* red = vp + hd;
     float* att_l = red + kAttnThreads + (4 - (3 * hd) % 4) % 4;  // 16-byte aligned for float4 reads
-    // scores held: the whole cache's, or a prompt pass's positions
-    const size_t seq4 = ((size_t)(a.batched ? a.batched : a.seq) + 3) & ~(size_t)3;
+    const size_t seq4 = ((size_t)a.seq + 3) & ~(size_t)3;
     float* att = a.att_g ? a.att_g + (size_t)h * seq4 : att_l;
     float* vt = a.att_g ? att_l : att_l + seq4;
     const int t0 = threadIdx.x;
@@ -265,13 +264,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     // (head_dim 64) thread t's cached k row t into registers.  Rows at or
     // past the position hold older values and are never used; rows past the
     // cache are not read.
-    // a prompt pass (a.batched positions): workgroup (h, p) reads row p of
-    // q | k | v and of the angle tables and writes row p of the output; the
-    // caller has already written every position's k and v to the cache
-    const int p = a.batched ? (int)blockIdx.y : *a.pos;
-    const float* qkv = a.batched ? a.qkv + (size_t)p * (dim + 2 * kv_dim) : a.qkv;
-    const float* cs = a.batched ? a.cs + (size_t)p * hd : a.cs;
-    float* out = a.batched ? a.out + (size_t)p * dim : a.out;
+    const int p = *a.pos;
+    const float* qkv = a.qkv;
+    const float* cs = a.cs;
+    float* out = a.out;
     float qv = 0.0f, kv = 0.0f, vv = 0.0f, rc = 0.0f, rs = 0.0f;
     if (t0 < hd) qv = qkv[h * hd + t0], kv = qkv[dim + hk * hd + t0], vv = qkv[dim + kv_dim + hk * hd + t0];
     if (t0 < hd / 2) rc = cs[2 * t0], rs = cs[2 * t0 + 1];
@@ -325,7 +321,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     __syncthreads();
     // the cache write, once per KV head; other heads of the group read
     // positions < pos from the cache and this position from kp / vp
-    if (!a.batched && h % kv_mul == 0) {
+    if (h % kv_mul == 0) {
         for (int d = t0; d < hd; d += kAttnThreads) {
             a.kc[(size_t)p * kv_dim + hk * hd + d] = kp[d];
             a.vc[(size_t)p * kv_dim + hk * hd + d] = vp[d];
@@ -450,6 +446,185 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     }
     __syncthreads();
     if (t0 < hd) out[h * hd + t0] = acc + att[p] * vp[t0];
+}
+
+// Orders one wave's LDS writes before its later LDS reads by other lanes:
+// a wave's LDS operations complete in issue order, so only the compiler has
+// to be kept from moving them across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Attention of a prompt pass: one wave per (query head, position); a
+// workgroup holds position blockIdx.y and G consecutive query heads of one KV
+// group (heads G * blockIdx.x + wave), which share that KV head's cached rows.
+// The arithmetic is attention_kernel's for its own position, step for step:
+// q (+ bias) with RoPE at position p's angles, each score a dot over d in
+// order, / sqrt(hd), the largest non-NaN score, expf, the serial sum over
+// positions 0..p, its reciprocal, the weights scaled by it, then per output
+// dim the weighted v rows summed over positions 0..p-1 in order, plus
+// position p's term.  The cached rows (rope_cache_kernel has written position
+// p's as well) go through one LDS tile of T rows, loaded by the whole
+// workgroup with coalesced 16-byte loads: k rows 0..p (lane r of a wave
+// scores row r of a tile, rows padded by 4 floats), then v rows 0..p-1 (lane
+// d adds dim d).  Each tile's loads are issued before the tile ahead of it is
+// used (the first k tile at the start, the first v tile before the softmax).
+// LDS: per wave q (hd floats) and the scores (P rounded up to 4), then the
+// tile.
+constexpr int kRowsMaxWaves = 8;
+constexpr int kRowsTileF4 = 4;  // float4 of a tile per thread
+__host__ __device__ inline int rows_tile(int G, int hd) { return kRowsTileF4 * G * 64 * 4 / hd; }
+__host__ __device__ inline int rows_tile_floats(int G, int hd) {
+    const int k = rows_tile(G, hd) * (hd + 4), v = kRowsTileF4 * G * 64 * 4;
+    return k > v ? k : v;
+}
+
+template <int HD>
+__global__ __launch_bounds__(kRowsMaxWaves * 64) void attention_rows_kernel(AttnArgs a) {
+    extern __shared__ float4 lds4[];
+    const int hd = HD > 0 ? HD : a.head_dim, lane = threadIdx.x & 63, wave = (int)(threadIdx.x >> 6);
+    const int G = (int)(blockDim.x >> 6), P = a.batched, nthr = (int)blockDim.x;
+    const int p = (int)blockIdx.y;
+    const int h = (int)blockIdx.x * G + wave, kv_mul = a.heads / a.kv_heads, hk = h / kv_mul;
+    const int kv_dim = a.kv_heads * hd, dim = a.heads * hd;
+    const int P4 = (P + 3) & ~3, T = rows_tile(G, hd), RS = hd + 4, H4 = hd / 4;
+    float* qs = reinterpret_cast<float*>(lds4) + (size_t)wave * (hd + P4);
+    float* att = qs + hd;
+    float* tile = reinterpret_cast<float*>(lds4) + (size_t)G * (hd + P4);
+    // rows c0 .. c0 + T - 1 below `end` of KV head hk of a cache: float4 i of
+    // the tile is row c0 + i / (hd/4), part i % (hd/4); other slots get an
+    // out-of-range offset (zeros, no memory traffic)
+    const size_t cbytes = (size_t)a.seq * kv_dim * 4;
+    const int nrec = (int)(cbytes < 0x7FFFFFF0u ? cbytes : 0x7FFFFFF0u);
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kc, (short)0, nrec, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vc, (short)0, nrec, 0x00020000);
+    float4 tr[kRowsTileF4];
+    auto load_rows = [&](__amdgpu_buffer_rsrc_t rs, int c0, int end) {
+#pragma unroll
+        for (int u = 0; u < kRowsTileF4; u++) {
+            const int i = (int)threadIdx.x + nthr * u, r = i / H4, t = c0 + r;
+            const uint32_t off = r < T && t < end ? (uint32_t)(((size_t)t * kv_dim + hk * hd) * 4 + 16 * (i % H4))
+                                                  : 0x80000000u;
+            tr[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+        }
+    };
+    // the loaded rows into the tile, row stride `stride` floats
+    auto store_rows = [&](int stride) {
+#pragma unroll
+        for (int u = 0; u < kRowsTileF4; u++) {
+            const int i = (int)threadIdx.x + nthr * u, r = i / H4;
+            if (r < T) reinterpret_cast<float4*>(tile + (size_t)r * stride)[i % H4] = tr[u];
+        }
+    };
+    load_rows(rk, 0, p + 1);
+    const float* qkv = a.qkv + (size_t)p * (dim + 2 * kv_dim);
+    const float* cs = a.cs + (size_t)p * hd;
+    for (int d = lane; d < hd; d += 64) {
+        float q = qkv[h * hd + d];
+        if (a.bq) q = q + a.bq[h * hd + d];
+        qs[d] = q;
+    }
+    wave_lds_sync();
+    for (int m = lane; m < hd / 2; m += 64) {
+        const float c = cs[2 * m], sn = cs[2 * m + 1];
+        const int i0 = a.neox ? m : 2 * m, i1 = a.neox ? m + hd / 2 : 2 * m + 1;
+        const float q0 = qs[i0], q1 = qs[i1];
+        qs[i0] = q0 * c - q1 * sn;
+        qs[i1] = q0 * sn + q1 * c;
+    }
+    wave_lds_sync();
+    const float sq = libm::sqrtf((float)hd);
+    float mx = -__builtin_inff();
+    for (int c0 = 0; c0 <= p; c0 += T) {  // uniform over the workgroup: every wave has this p
+        store_rows(RS);
+        __syncthreads();
+        if (c0 + T <= p) load_rows(rk, c0 + T, p + 1);
+        const int nt = p + 1 - c0 < T ? p + 1 - c0 : T;
+        for (int r = lane; r < nt; r += 64) {
+            const float4* kt = reinterpret_cast<const float4*>(tile + (size_t)r * RS);
+            const float4* q4 = reinterpret_cast<const float4*>(qs);
+            float score = 0.0f;
+            if constexpr (HD > 0) {
+#pragma unroll
+                for (int j = 0; j < HD / 4; j++) {
+                    const float4 qv = q4[j], kv = kt[j];
+                    score += qv.x * kv.x;
+                    score += qv.y * kv.y;
+                    score += qv.z * kv.z;
+                    score += qv.w * kv.w;
+                }
+            } else {
+                for (int j = 0; j < H4; j++) {
+                    const float4 qv = q4[j], kv = kt[j];
+                    score += qv.x * kv.x;
+                    score += qv.y * kv.y;
+                    score += qv.z * kv.z;
+                    score += qv.w * kv.w;
+                }
+            }
+            score /= sq;
+            att[c0 + r] = score;
+            if (score > mx) mx = score;  // a NaN score never becomes the max
+        }
+        __syncthreads();
+    }
+    load_rows(rv, 0, p);  // the first v tile, in flight during the softmax
+    mx = wave_max_nonneg(mx);  // exact for any non-NaN values
+    for (int t = lane; t <= p; t += 64) att[t] = libm::expf(att[t] - mx);
+    wave_lds_sync();
+    const float inv = 1.0f / serial_sum_wave(att, p + 1);
+    wave_lds_sync();
+    for (int t = lane; t <= p; t += 64) att[t] *= inv;
+    wave_lds_sync();
+    // out[d] for d = lane + 64 s (s < hd/64 rounded up)
+    constexpr int kS = HD > 0 ? (HD + 63) / 64 : 4;
+    float acc[kS];
+#pragma unroll
+    for (int sl = 0; sl < kS; sl++) acc[sl] = 0.0f;
+    for (int c0 = 0; c0 < p; c0 += T) {  // uniform over the workgroup
+        store_rows(hd);
+        __syncthreads();
+        if (c0 + T < p) load_rows(rv, c0 + T, p);
+        const int nt = p - c0 < T ? p - c0 : T;
+#pragma unroll
+        for (int sl = 0; sl < kS; sl++) {
+            const int d = lane + 64 * sl;
+            if (d < hd) {
+                float s_acc = acc[sl];
+                int t = 0;
+                for (; t + 8 <= nt; t += 8) {
+                    float vb[8], ab[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) vb[j] = tile[(t + j) * hd + d];
+                    const float4 w0 = *reinterpret_cast<const float4*>(att + c0 + t);
+                    const float4 w1 = *reinterpret_cast<const float4*>(att + c0 + t + 4);
+                    ab[0] = w0.x, ab[1] = w0.y, ab[2] = w0.z, ab[3] = w0.w;
+                    ab[4] = w1.x, ab[5] = w1.y, ab[6] = w1.z, ab[7] = w1.w;
+                    float pr[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) pr[j] = ab[j] * vb[j];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) s_acc += pr[j];
+                }
+                for (; t < nt; t++) s_acc += att[c0 + t] * tile[t * hd + d];
+                acc[sl] = s_acc;
+            }
+        }
+        __syncthreads();
+    }
+    const float* vrow = qkv + dim + kv_dim + hk * hd;
+    float* out = a.out + (size_t)p * dim + h * hd;
+#pragma unroll
+    for (int sl = 0; sl < kS; sl++) {
+        const int d = lane + 64 * sl;
+        if (d < hd) {
+            float v = vrow[d];
+            if (a.bv) v = v + a.bv[hk * hd + d];
+            out[d] = acc[sl] + att[p] * v;
+        }
+    }
 }
 
 // The cache write of a prompt pass: workgroup (p, hk) writes position p's
@@ -625,9 +800,8 @@ hipError_t rms_norm_rows(const float* x, const float* w, int n, int rows, float 
 template <int HD>
 static hipError_t launch_attention(const AttnArgs& a, size_t lds, hipStream_t stream) {
     if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(attention_kernel<HD>), lds)) return e;
-    const int extra = a.batched ? 0 : a.pf.groups;
-    hipLaunchKernelGGL(attention_kernel<HD>, dim3((unsigned)(a.heads + extra), (unsigned)(a.batched ? a.batched : 1)),
-                       dim3(kAttnThreads), lds, stream, a);
+    hipLaunchKernelGGL(attention_kernel<HD>, dim3((unsigned)(a.heads + a.pf.groups)), dim3(kAttnThreads), lds, stream,
+                       a);
     return hipGetLastError();
 }
 
@@ -637,12 +811,42 @@ static size_t attention_lds(int head_dim, int seq, bool scores) {
             kAttnTile * 64) * 4;
 }
 
-// a prompt pass of P positions: P scores, and P cached v rows where the
-// head-dim-64 path holds them all (else the tiles)
-static size_t attention_lds_rows(int head_dim, int P) {
-    const bool fast = head_dim == 64 && P <= kAttnThreads;
-    return ((size_t)3 * head_dim + kAttnThreads + 4 + (((size_t)P + 3) & ~(size_t)3) +
-            (fast ? (size_t)P * head_dim : (size_t)kAttnTile * 64)) * 4;
+// a prompt pass: G query heads (waves) per workgroup, the largest divisor
+// of the KV group size up to kRowsMaxWaves whose q and score rows fit in
+// LDS; 0 if none does
+static size_t attention_rows_lds(int head_dim, int P, int G) {
+    return ((size_t)G * ((size_t)head_dim + (((size_t)P + 3) & ~(size_t)3)) + (size_t)rows_tile_floats(G, head_dim)) * 4;
+}
+
+static int attention_rows_waves(int head_dim, int P, int kv_mul) {
+    for (int G = kv_mul < kRowsMaxWaves ? kv_mul : kRowsMaxWaves; G >= 1; G--)
+        if (kv_mul % G == 0 && attention_rows_lds(head_dim, P, G) <= 160 * 1024 && rows_tile(G, head_dim) >= 1)
+            return G;
+    return 0;
+}
+
+template <int HD>
+static hipError_t launch_attention_rows(const AttnArgs& a, int G, hipStream_t stream) {
+    const size_t lds = attention_rows_lds(a.head_dim, a.batched, G);
+    if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(attention_rows_kernel<HD>), lds)) return e;
+    hipLaunchKernelGGL(attention_rows_kernel<HD>, dim3((unsigned)(a.heads / G), (unsigned)a.batched),
+                       dim3((unsigned)G * 64), lds, stream, a);
+    return hipGetLastError();
+}
+
+bool attention_rows_supported(int head_dim, int P, int heads, int kv_heads) {
+    return head_dim > 0 && head_dim <= 256 && head_dim % 4 == 0 && P > 0 && kv_heads > 0 && heads % kv_heads == 0 &&
+           attention_rows_waves(head_dim, P, heads / kv_heads) > 0;
+}
+
+static hipError_t attention_rows(const AttnArgs& a, hipStream_t stream) {
+    if (a.batched > a.seq || !attention_rows_supported(a.head_dim, a.batched, a.heads, a.kv_heads))
+        return hipErrorInvalidValue;
+    const int G = attention_rows_waves(a.head_dim, a.batched, a.heads / a.kv_heads);
+    if (!G) return hipErrorInvalidValue;
+    if (a.head_dim == 64) return launch_attention_rows<64>(a, G, stream);
+    if (a.head_dim == 128) return launch_attention_rows<128>(a, G, stream);
+    return launch_attention_rows<0>(a, G, stream);
 }
 
 bool attention_supported(int head_dim, int seq) {
@@ -656,10 +860,9 @@ bool attention_scores_in_lds(int head_dim, int seq) {
 
 hipError_t attention(const AttnArgs& a, hipStream_t stream) {
     if (!attention_supported(a.head_dim, a.seq)) return hipErrorInvalidValue;
+    if (a.batched) return attention_rows(a, stream);
     const bool in_lds = attention_scores_in_lds(a.head_dim, a.seq);
     if (!in_lds && !a.att_g) return hipErrorInvalidValue;
-    // a prompt pass keeps every workgroup's scores in its own LDS
-    if (a.batched && (!in_lds || a.batched < 0 || a.batched > a.seq)) return hipErrorInvalidValue;
     const AttnArgs* ap = &a;
     AttnArgs lds_args;
     if (in_lds && a.att_g) {  // the scores fit: keep them in LDS
@@ -667,7 +870,7 @@ hipError_t attention(const AttnArgs& a, hipStream_t stream) {
         lds_args.att_g = nullptr;
         ap = &lds_args;
     }
-    const size_t lds = a.batched ? attention_lds_rows(a.head_dim, a.batched) : attention_lds(a.head_dim, a.seq, in_lds);
+    const size_t lds = attention_lds(a.head_dim, a.seq, in_lds);
     if (a.head_dim == 64) return launch_attention<64>(*ap, lds, stream);
     if (a.head_dim == 128) return launch_attention<128>(*ap, lds, stream);
     return launch_attention<0>(*ap, lds, stream);

@@ -1089,10 +1089,10 @@ int run_impl(vtqrt_model* m, int regime, const char* model_id, const uint8_t wei
         }
         if (graph) (void)hipGraphDestroy(graph);
     }
-    // the prompt at once where the recorders are off and every position's
-    // scores fit in LDS; else step by step from position 0
+    // the prompt at once where the recorders are off and its attention fits
+    // the prompt-pass kernel; else step by step from position 0
     const bool batched = !rec && m->prompt_mode == VTQRT_PROMPT_BATCHED && prompt_len >= 2 &&
-                         vtq::decode::attention_scores_in_lds(head, m->seq);
+                         vtq::decode::attention_rows_supported(head, prompt_len, m->heads, m->kv_heads);
     int pos0 = 0;
     if (batched) {
         rc = enqueue_prefill(m, regime, prompt_len, total, hist);
