@@ -95,6 +95,22 @@ def test_e2e_context_beyond_lds_scores():
     compare(LONG_CTX, 280, 10, regimes=(0,), threads=16)
 
 
+# Head dims other than 64 and 128 take both attention kernels' generic
+# instantiations.  32 with eight query heads per KV head: the prompt pass's
+# workgroups of 8 waves use 256-row tiles of the cache, which a 300-position
+# prompt crosses.  256 with two query heads per KV head (qwen2: NeoX pairs
+# and biases): 2-wave workgroups and 8-row tiles.
+HD32 = dict(dim=256, hidden=512, layers=2, heads=8, kv_heads=1, vocab=1000, ctx=320, rope_theta=10000.0,
+            rms_eps=1e-5)
+HD256 = dict(dim=512, hidden=512, layers=2, heads=2, kv_heads=1, vocab=1000, ctx=48, rope_theta=10000.0,
+             rms_eps=1e-5)
+
+
+def test_e2e_generic_head_dims():
+    compare(HD32, 300, 6, regimes=(0,), threads=16)
+    compare(HD256, 30, 8, regimes=(0,), arch="qwen2", qkv_bias=True)
+
+
 def test_e2e_walk_row_bounds():
     compare(WALK_LO, 5, 9, regimes=(0,))
     compare(WALK_HI, 5, 9, regimes=(0,), threads=16)
