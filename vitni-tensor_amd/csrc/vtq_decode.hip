@@ -275,26 +275,35 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float4 kr[KPT], vr[KPT];
     const bool fast = kFast && p < kAttnThreads;
     if constexpr (kFast) {
-        // cached rows 0..pos-1 (fast path): thread t's k row t, and float4
-        // i = t0 + kAttnThreads*u of the head's v rows, as raw buffer loads
-        // whose unneeded slots get an out-of-range offset (zeros, no memory
+        // cached rows 0..pos-1 (fast path): float4 i = t0 + kAttnThreads*u
+        // of the head's k rows and of its v rows (row i / 16, part i % 16:
+        // each load instruction reads whole rows), as raw buffer loads whose
+        // unneeded slots get an out-of-range offset (zeros, no memory
         // traffic), so every load is unconditional and the wait counts stay
-        // exact
+        // exact.  The k rows then go through the v tile's LDS, so that thread
+        // t can read row t for its score.
         const size_t cbytes = (size_t)a.seq * kv_dim * 4;
         const int nrec = (int)(cbytes < 0x7FFFFFF0u ? cbytes : 0x7FFFFFF0u);
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kc, (short)0, nrec, 0x00020000);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vc, (short)0, nrec, 0x00020000);
-        const uint32_t koff = fast && t0 < p ? (uint32_t)(((size_t)t0 * kv_dim + hk * hd) * 4) : 0x80000000u;
-#pragma unroll
-        for (int j = 0; j < KPT; j++)
-            kr[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, koff + 16 * j, 0, 0));
         const int nv = fast ? p * (HD / 4) : 0;
 #pragma unroll
         for (int u = 0; u < KPT; u++) {
             const int i = t0 + kAttnThreads * u, t = i / (HD / 4);
             const uint32_t off = i < nv ? (uint32_t)(((size_t)t * kv_dim + hk * hd) * 4 + 16 * (i % (HD / 4)))
                                         : 0x80000000u;
+            kr[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
             vr[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+        }
+        // row t's part j at float4 16t + (j ^ (t % 16)) of the tile: a row's
+        // sixteen writes and sixteen threads' reads of one part each cover
+        // all banks
+        if (fast) {
+#pragma unroll
+            for (int u = 0; u < KPT; u++) {
+                const int i = t0 + kAttnThreads * u, t = i / (HD / 4);
+                if (i < nv) reinterpret_cast<float4*>(vt)[16 * t + ((i % (HD / 4)) ^ (t & 15))] = kr[u];
+            }
         }
     }
     for (int d = t0; d < hd; d += kAttnThreads) {
@@ -332,10 +341,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float mx = -__builtin_inff();
     if (fast) {
         if (t0 <= p) {
-            // position p's k is this step's roped k (LDS), the others' the cached row
+            // position p's k is this step's roped k (LDS), the others' the
+            // cached row (in the tile)
             if (t0 == p) {
 #pragma unroll
                 for (int j = 0; j < KPT; j++) kr[j] = reinterpret_cast<const float4*>(kp)[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < KPT; j++) kr[j] = reinterpret_cast<const float4*>(vt)[16 * t0 + (j ^ (t0 & 15))];
             }
             float score = 0.0f;
 #pragma unroll
