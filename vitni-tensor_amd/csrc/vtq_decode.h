@@ -36,6 +36,10 @@ hipError_t embed(int ggml_type, const uint8_t* table, uint32_t rows, const uint3
 hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out, hipStream_t stream);
 // the same for `rows` rows of n floats (row r of x into row r of out)
 hipError_t rms_norm_rows(const float* x, const float* w, int n, int rows, float eps, float* out, hipStream_t stream);
+// the residual first: x[i] = x[i] + add[i] over the rows (as add_inplace),
+// then rms_norm_rows of the updated x; add == nullptr: rms_norm_rows
+hipError_t add_rms_norm_rows(float* x, const float* add, const float* w, int n, int rows, float eps, float* out,
+                             hipStream_t stream);
 
 // Byte ranges later kernels of the step read, streamed through the
 // memory-side cache by `groups` extra workgroups of the attention launch

@@ -136,11 +136,26 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(int type, const uint8_t
 // by wave 0: where the walk of vtq_sumsq.h applies (1024-4096 terms, a
 // multiple of 64) with the products in its pass layout and waves 1-3 as its
 // helpers, otherwise as one chain over the products in order
-__global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int n,
-                                                       float eps, float* __restrict__ out) {
-    // one row per workgroup (rows of n floats, row blockIdx.x)
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float* x, const float* __restrict__ add, float* xw,
+                                                       const float* __restrict__ w, int n, float eps,
+                                                       float* __restrict__ out) {
+    // one row per workgroup (rows of n floats, row blockIdx.x); with add,
+    // the row is x + add (a residual, x[i] + add[i] per element), written to
+    // xw (which may be x) and normalised
     x += (size_t)blockIdx.x * n;
     out += (size_t)blockIdx.x * n;
+    if (add) {
+        add += (size_t)blockIdx.x * n;
+        xw += (size_t)blockIdx.x * n;
+    }
+    auto elem = [&](int i) {
+        float v = x[i];
+        if (add) {
+            v = v + add[i];
+            xw[i] = v;
+        }
+        return v;
+    };
     extern __shared__ float4 prod4[];
     float* prod = reinterpret_cast<float*>(prod4);
     __shared__ float scale_s;
@@ -150,7 +165,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
         SumsqWalk& walk = *reinterpret_cast<SumsqWalk*>(prod + 4096);
         float hpart = 0.0f, apart = 0.0f;
         for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            const float p = x[i] * x[i];
+            const float v = elem(i);
+            const float p = v * v;
             prod[sumsq_pass_index(i)] = p;
             apart += p;
             if (i < H) hpart += p;
@@ -173,7 +189,10 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
             if (threadIdx.x == 0) scale_s = 1.0f / libm::sqrtf(mean + eps);
         }
     } else {
-        for (int i = threadIdx.x; i < n; i += blockDim.x) prod[i] = x[i] * x[i];
+        for (int i = threadIdx.x; i < n; i += blockDim.x) {
+            const float v = elem(i);
+            prod[i] = v * v;
+        }
         __syncthreads();
         if (threadIdx.x < 64) {
             const float sumsq = serial_sum_wave(prod, n);
@@ -183,7 +202,8 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float* __restrict__
     }
     __syncthreads();
     const float scale = scale_s;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * scale * w[i];
+    const float* xs = add ? xw : x;  // each thread reads back only what it wrote
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = xs[i] * scale * w[i];
 }
 
 // A prefetch workgroup: workgroup g of G streams its share of every range
@@ -798,15 +818,21 @@ hipError_t rms_norm(const float* x, const float* w, int n, float eps, float* out
     // products in order (the serial sum reads whole float4s)
     const size_t lds = sumsq_walk_head(n) ? 4096 * 4 + sizeof(SumsqWalk) : (size_t)((n + 3) & ~3) * 4;
     if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(rms_norm_kernel), lds)) return e;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(256), lds, stream, x, w, n, eps, out);
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(256), lds, stream, x, nullptr, nullptr, w, n, eps, out);
     return hipGetLastError();
 }
 
 hipError_t rms_norm_rows(const float* x, const float* w, int n, int rows, float eps, float* out, hipStream_t stream) {
+    return add_rms_norm_rows(const_cast<float*>(x), nullptr, w, n, rows, eps, out, stream);
+}
+
+hipError_t add_rms_norm_rows(float* x, const float* add, const float* w, int n, int rows, float eps, float* out,
+                             hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
     const size_t lds = sumsq_walk_head(n) ? 4096 * 4 + sizeof(SumsqWalk) : (size_t)((n + 3) & ~3) * 4;
     if (hipError_t e = allow_dynamic_lds(reinterpret_cast<const void*>(rms_norm_kernel), lds)) return e;
-    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)rows), dim3(256), lds, stream, x, w, n, eps, out);
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)rows), dim3(256), lds, stream, x, add, add ? x : nullptr, w, n,
+                       eps, out);
     return hipGetLastError();
 }
 

@@ -463,10 +463,13 @@ int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
                                              hipMemcpyDeviceToDevice, m->stream),
                          "q|k|v rows");
     };
+    // the previous layer's W2 rows, added to x by the next norm (residual)
+    const float* pend = nullptr;
     for (int l = 0; !rc && l < m->layers; l++) {
         const Layer& Ly = m->L[l];
-        // q | k | v = W (rms_norm(x, attn_norm)), one row per position
-        rc = hip_check(m, dec::rms_norm_rows(X, f32_at(m, Ly.rms_att), dim, P, m->eps, XN, m->stream), "rms_norm");
+        // q | k | v = W (rms_norm(x + residual, attn_norm)), one row per position
+        rc = hip_check(m, dec::add_rms_norm_rows(X, pend, f32_at(m, Ly.rms_att), dim, P, m->eps, XN, m->stream),
+                       "rms_norm");
         if (rc) break;
         const bool joint = Ly.wk.type == Ly.wq.type && Ly.wv.type == Ly.wq.type &&
                            Ly.wk.dev == Ly.wq.dev + Ly.wq.nbytes && Ly.wv.dev == Ly.wk.dev + Ly.wk.nbytes;
@@ -506,9 +509,10 @@ int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
             break;
         // x = x + Wo att
         rc = linear_rows(m, regime, Ly.wo.type, m->dblob + Ly.wo.dev, Ly.wo.nbytes, ATT, P, dim, dim, TMP);
-        if (!rc) rc = hip_check(m, dec::add_inplace(X, TMP, P * dim, m->stream), "residual");
-        // ffn = silu(W1 h) * (W3 h), h = rms_norm(x, ffn_norm)
-        if (!rc) rc = hip_check(m, dec::rms_norm_rows(X, f32_at(m, Ly.rms_ffn), dim, P, m->eps, XN, m->stream), "rms_norm");
+        // ffn = silu(W1 h) * (W3 h), h = rms_norm(x, ffn_norm), with the residual
+        if (!rc)
+            rc = hip_check(m, dec::add_rms_norm_rows(X, TMP, f32_at(m, Ly.rms_ffn), dim, P, m->eps, XN, m->stream),
+                           "rms_norm");
         if (!rc && Ly.w3.type == Ly.w1.type && Ly.w3.dev == Ly.w1.dev + Ly.w1.nbytes) {
             // gate | up rows from one linear of 2 * hidden rows (G and U back to back)
             rc = linear_rows(m, regime, Ly.w1.type, m->dblob + Ly.w1.dev, Ly.w1.nbytes + Ly.w3.nbytes, XN, P, dim,
@@ -520,8 +524,9 @@ int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
             if (!rc) rc = hip_check(m, dec::swiglu(G, U, F, P * hidden, m->stream), "swiglu");
         }
         // x = x + W2 ffn
+        // (the residual add is the next norm's: the next layer's or the final one)
         if (!rc) rc = linear_rows(m, regime, Ly.w2.type, m->dblob + Ly.w2.dev, Ly.w2.nbytes, F, P, hidden, dim, TMP);
-        if (!rc) rc = hip_check(m, dec::add_inplace(X, TMP, P * dim, m->stream), "residual");
+        pend = TMP;
     }
     if (rc) return rc;
     // logits = W_out (rms_norm(x, output_norm)): every position's into hist,
@@ -529,12 +534,15 @@ int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
     const Lin& head_w = m->shared ? m->tok : m->wcls;
     const float* lg = m->logits;
     if (hist) {
-        rc = hip_check(m, dec::rms_norm_rows(X, f32_at(m, m->rms_final), dim, P, m->eps, XN, m->stream), "rms_norm");
+        rc = hip_check(m, dec::add_rms_norm_rows(X, pend, f32_at(m, m->rms_final), dim, P, m->eps, XN, m->stream),
+                       "rms_norm");
         if (!rc) rc = linear_rows(m, regime, head_w.type, m->dblob + head_w.dev, head_w.nbytes, XN, P, dim, m->vocab, hist);
         lg = hist + (size_t)(P - 1) * m->vocab;
     } else {
-        rc = hip_check(m, dec::rms_norm(X + (size_t)(P - 1) * dim, f32_at(m, m->rms_final), dim, m->eps, m->xb,
-                                        m->stream),
+        // position P-1's row alone (the other rows' last residual is not needed)
+        const size_t r = (size_t)(P - 1) * dim;
+        rc = hip_check(m, dec::add_rms_norm_rows(X + r, pend ? pend + r : nullptr, f32_at(m, m->rms_final), dim, 1,
+                                                 m->eps, m->xb, m->stream),
                        "rms_norm");
         if (!rc) rc = linear(m, regime, head_w, m->xb, dim, m->vocab, m->logits);
     }
