@@ -13,14 +13,16 @@
 namespace vtq {
 namespace decode {
 
-// This step's RoPE angles (cos, sin) per pair m < head_dim/2, written to
-// cs[2m], cs[2m+1] by the kernel that prepares the step (embed for the
-// first, argmax_advance for the next), read by attention.
+// The RoPE angle table: position q's (cos, sin) of pair m < head_dim/2 at
+// cs[q * head_dim + 2m], +1 (rope_table, forward_quantized.rs:417-456).  It
+// depends on the position alone, so rope_table_rows fills it once per model
+// for every position of the cache; attention reads row *pos.
 struct RopeArgs {
-    float* cs;  // nullptr: not written
+    float* cs;
     int head_dim;
     float theta;
 };
+hipError_t rope_table_rows(const RopeArgs& r, int rows, hipStream_t stream);
 
 // embedding_row (src/model/forward_quantized.rs:818-923): row tokens[*pos]
 // of the table (ggml type 0, 2, 6, 8, 12 or 14, `rows` rows) into x[0..dim);
@@ -29,7 +31,7 @@ struct RopeArgs {
 // that is not a whole number of blocks.
 size_t embed_row_bytes(int ggml_type, int dim);
 hipError_t embed(int ggml_type, const uint8_t* table, uint32_t rows, const uint32_t* tokens, const int* pos, int dim,
-                 float* x, const RopeArgs& rope, hipStream_t stream);
+                 float* x, hipStream_t stream);
 
 // rms_norm_slice (src/ops/rms_norm.rs:60-110): out = x * scale * w with the
 // sum of squares accumulated serially, as the reference does.
@@ -64,7 +66,7 @@ struct AttnArgs {
     const float* qkv;            // q[dim] | k[kv_dim] | v[kv_dim] of this step
     const float *bq, *bk, *bv;   // optional biases (added before RoPE / the cache write)
     float *kc, *vc;              // this layer's caches, [seq][kv_dim]
-    const float* cs;             // this step's RoPE angles (RopeArgs)
+    const float* cs;             // the RoPE angle table (RopeArgs): row p is position p's
     float* out;                  // [dim] attention output (the Wo input)
     const int* pos;
     int heads, kv_heads, head_dim, seq;
@@ -95,10 +97,9 @@ bool attention_rows_supported(int head_dim, int P, int heads, int kv_heads);
 // The prompt pass's cache write: position p's k (bias, RoPE) and v for
 // p < a.batched, as attention computes them for its own position.
 hipError_t rope_cache_rows(const AttnArgs& a, hipStream_t stream);
-// embedding_row of tokens[0..P) into x[P][dim], and position p's RoPE angles
-// into rope.cs[p * head_dim ..] (when rope.cs is set)
+// embedding_row of tokens[0..P) into x[P][dim]
 hipError_t embed_rows(int ggml_type, const uint8_t* table, uint32_t rows, const uint32_t* tokens, int P, int dim,
-                      float* x, const RopeArgs& rope, hipStream_t stream);
+                      float* x, hipStream_t stream);
 
 // The embedding table, for the next step's row (see embed).
 struct EmbedArgs {
@@ -108,7 +109,6 @@ struct EmbedArgs {
     size_t row_bytes;
     int dim;
     float* x;
-    RopeArgs rope;  // the next step's angles
 };
 
 // argmax_last_dim (src/ops/argmax.rs:21-68) of logits[0..vocab): the next

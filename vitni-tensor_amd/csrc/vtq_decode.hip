@@ -105,27 +105,28 @@ __device__ void rope_table(const RopeArgs& r, int q) {
     }
 }
 
+// the angle table's rows 0..rows-1: workgroup q writes position q's
+__global__ __launch_bounds__(128) void rope_rows_kernel(RopeArgs r) {
+    const int q = (int)blockIdx.x;
+    RopeArgs rq = r;
+    rq.cs = r.cs + (size_t)q * r.head_dim;
+    rope_table(rq, q);
+}
+
 // a token past the table reads row 0 (the host reports the reference's error)
 __global__ __launch_bounds__(256) void embed_kernel(int type, const uint8_t* __restrict__ table, uint32_t rows,
                                                     const uint32_t* __restrict__ tokens, const int* __restrict__ pos,
-                                                    int dim, size_t rb, float* __restrict__ x, RopeArgs rope) {
-    if (rope.cs) rope_table(rope, *pos);
+                                                    int dim, size_t rb, float* __restrict__ x) {
     const uint32_t tok = tokens[*pos];
     const uint8_t* row = table + (size_t)(tok < rows ? tok : 0u) * rb;
     for (int i = threadIdx.x; i < dim; i += blockDim.x) x[i] = embed_elem(type, row, i);
 }
 
-// the prompt's rows at once: workgroup p embeds tokens[p] into x[p][..] and
-// writes position p's RoPE angles to cs[p * head_dim ..]
+// the prompt's rows at once: workgroup p embeds tokens[p] into x[p][..]
 __global__ __launch_bounds__(256) void embed_rows_kernel(int type, const uint8_t* __restrict__ table, uint32_t rows,
                                                          const uint32_t* __restrict__ tokens, int dim, size_t rb,
-                                                         float* __restrict__ x, RopeArgs rope) {
+                                                         float* __restrict__ x) {
     const int p = (int)blockIdx.x;
-    if (rope.cs) {
-        RopeArgs rp = rope;
-        rp.cs = rope.cs + (size_t)p * rope.head_dim;
-        rope_table(rp, p);
-    }
     const uint32_t tok = tokens[p];
     const uint8_t* row = table + (size_t)(tok < rows ? tok : 0u) * rb;
     float* xp = x + (size_t)p * dim;
@@ -286,7 +287,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     // cache are not read.
     const int p = *a.pos;
     const float* qkv = a.qkv;
-    const float* cs = a.cs;
+    const float* cs = a.cs + (size_t)p * hd;
     float* out = a.out;
     float qv = 0.0f, kv = 0.0f, vv = 0.0f, rc = 0.0f, rs = 0.0f;
     if (t0 < hd) qv = qkv[h * hd + t0], kv = qkv[dim + hk * hd + t0], vv = qkv[dim + kv_dim + hk * hd + t0];
@@ -762,7 +763,6 @@ __global__ __launch_bounds__(kArgThreads) void argmax_kernel(const float* __rest
         *pos = p + 1;
     }
     __syncthreads();
-    if (p + 1 < total && e.rope.cs) rope_table(e.rope, p + 1);
     if (p + 1 < total && e.table) {
         const uint32_t tok = next_s;
         const uint8_t* row = e.table + (size_t)(tok < e.rows ? tok : 0u) * e.row_bytes;
@@ -807,9 +807,9 @@ size_t embed_row_bytes(int ggml_type, int dim) {
 }
 
 hipError_t embed(int ggml_type, const uint8_t* table, uint32_t rows, const uint32_t* tokens, const int* pos, int dim,
-                 float* x, const RopeArgs& rope, hipStream_t stream) {
+                 float* x, hipStream_t stream) {
     hipLaunchKernelGGL(embed_kernel, dim3(1), dim3(256), 0, stream, ggml_type, table, rows, tokens, pos, dim,
-                       row_bytes(ggml_type, dim), x, rope);
+                       row_bytes(ggml_type, dim), x);
     return hipGetLastError();
 }
 
@@ -916,10 +916,17 @@ hipError_t attention(const AttnArgs& a, hipStream_t stream) {
 }
 
 hipError_t embed_rows(int ggml_type, const uint8_t* table, uint32_t rows, const uint32_t* tokens, int P, int dim,
-                      float* x, const RopeArgs& rope, hipStream_t stream) {
+                      float* x, hipStream_t stream) {
     if (P <= 0) return hipSuccess;
     hipLaunchKernelGGL(embed_rows_kernel, dim3((unsigned)P), dim3(256), 0, stream, ggml_type, table, rows, tokens, dim,
-                       row_bytes(ggml_type, dim), x, rope);
+                       row_bytes(ggml_type, dim), x);
+    return hipGetLastError();
+}
+
+hipError_t rope_table_rows(const RopeArgs& r, int rows, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    if (!r.cs || r.head_dim <= 0) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rope_rows_kernel, dim3((unsigned)rows), dim3(128), 0, stream, r);
     return hipGetLastError();
 }
 

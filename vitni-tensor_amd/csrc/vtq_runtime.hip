@@ -285,13 +285,14 @@ int norm_to_xb(vtqrt_model* m, const Lin& w) {
     return hip_check(m, vtq::decode::rms_norm(m->x, f32_at(m, w), m->dim, m->eps, m->xb, m->stream), "rms_norm");
 }
 
+// the RoPE angle table, one row per position of the cache
 vtq::decode::RopeArgs rope_args(vtqrt_model* m) {
     return vtq::decode::RopeArgs{m->rope, m->dim / m->heads, m->theta};
 }
 
 vtq::decode::EmbedArgs embed_args(vtqrt_model* m) {
     return vtq::decode::EmbedArgs{m->tok.type, m->dblob + m->tok.dev, table_rows(m),
-                                  vtq::decode::embed_row_bytes(m->tok.type, m->dim), m->dim, m->x, rope_args(m)};
+                                  vtq::decode::embed_row_bytes(m->tok.type, m->dim), m->dim, m->x};
 }
 
 // a range for the attention launch's prefetch workgroups; row_bytes nonzero:
@@ -415,8 +416,8 @@ int enqueue_step(vtqrt_model* m, int regime, int prompt_len, int total, float* h
 }
 
 // The prompt pass: positions 0 .. P-1 of forward_quantized::step at once,
-// then step P-1's argmax (which writes tokens[P], the next step's embedding
-// row and angles, and advances *pos to P).  Every linear takes the P rows as
+// then step P-1's argmax (which writes tokens[P] and the next step's
+// embedding row, and advances *pos to P).  Every linear takes the P rows as
 // one batch (the prefill GEMM for Q4_K), and batch rows are independent, so
 // each position's activations, cache rows and logits are those of its own
 // step: the same kernels' arithmetic per row (RMSNorm per row, the cache
@@ -429,9 +430,8 @@ int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
     const int qw = dim + 2 * kv_dim;
     auto al = [](size_t n) { return (n + 63) / 64 * 64; };
     const size_t Pz = (size_t)P;
-    const size_t nX = al(Pz * dim), nQKV = al(Pz * qw), nH = al(Pz * hidden), nCS = al(Pz * head),
-                 nK = al(Pz * kv_dim);
-    const size_t need = 5 * nX + nQKV + 3 * nH + nCS + 2 * nK;
+    const size_t nX = al(Pz * dim), nQKV = al(Pz * qw), nH = al(Pz * hidden), nK = al(Pz * kv_dim);
+    const size_t need = 5 * nX + nQKV + 3 * nH + 2 * nK;
     int rc = VTQ_OK;
     if (m->pf_cap < need) {
         if (m->pf) (void)hipFree(m->pf);
@@ -449,12 +449,9 @@ int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
     float* G = QKV + nQKV;
     float* U = G + nH;
     float* F = U + nH;
-    float* CS = F + nH;
-    float* KB = CS + nCS;
+    float* KB = F + nH;
     float* VB = KB + nK;
-    dec::RopeArgs ra = rope_args(m);
-    ra.cs = CS;
-    if ((rc = hip_check(m, dec::embed_rows(m->tok.type, m->dblob + m->tok.dev, table_rows(m), m->tokens, P, dim, X, ra,
+    if ((rc = hip_check(m, dec::embed_rows(m->tok.type, m->dblob + m->tok.dev, table_rows(m), m->tokens, P, dim, X,
                                            m->stream),
                         "embedding_row")))
         return rc;
@@ -493,7 +490,7 @@ int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
         a.bv = f32_at(m, Ly.bv);
         a.kc = m->kc + (size_t)l * m->seq * kv_dim;
         a.vc = m->vc + (size_t)l * m->seq * kv_dim;
-        a.cs = CS;
+        a.cs = m->rope;
         a.out = ATT;
         a.pos = m->pos;
         a.heads = m->heads;
@@ -547,7 +544,7 @@ int enqueue_prefill(vtqrt_model* m, int regime, int P, int total, float* hist) {
         if (!rc) rc = linear(m, regime, head_w, m->xb, dim, m->vocab, m->logits);
     }
     if (rc) return rc;
-    // step P-1's argmax: tokens[P], the next step's row and angles, *pos = P
+    // step P-1's argmax: tokens[P], the next step's row, *pos = P
     if ((rc = hip_check(m, hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(m->pos), P - 1, 1, m->stream),
                         "position")))
         return rc;
@@ -948,8 +945,12 @@ int vtqrt_load(int device, const uint8_t* gguf, size_t len, vtqrt_model** out) {
         (rc = dalloc(&m->att, m->dim)) || (rc = dalloc(&m->ffn, m->hidden)) || (rc = dalloc(&m->gate, m->hidden)) ||
         (rc = dalloc(&m->up, m->hidden)) || (rc = dalloc(&m->tmp, m->dim)) || (rc = dalloc(&m->logits, m->vocab)) ||
         (rc = dalloc(&m->kc, kv_elems)) || (rc = dalloc(&m->vc, kv_elems)) ||
-        (rc = dalloc(&m->tokens, (size_t)m->seq + 1)) || (rc = dalloc(&m->pos, 1)) || (rc = dalloc(&m->rope, head)) ||
+        (rc = dalloc(&m->tokens, (size_t)m->seq + 1)) || (rc = dalloc(&m->pos, 1)) ||
+        (rc = dalloc(&m->rope, (size_t)m->seq * (size_t)std::max(head, 1))) ||
         (rc = dalloc(&m->pf_sink, 64)))
+        return rc;
+    // the RoPE angles of every position, once (rope_table)
+    if (head > 0 && (rc = hip_check(m, vtq::decode::rope_table_rows(rope_args(m), m->seq, m->stream), "rope table")))
         return rc;
     // a context too long for the attention kernel's LDS keeps each head's
     // scores in a row of HBM
@@ -1107,7 +1108,7 @@ int run_impl(vtqrt_model* m, int regime, const char* model_id, const uint8_t wei
         pos0 = prompt_len;
     } else {
         rc = hip_check(m, vtq::decode::embed(m->tok.type, m->dblob + m->tok.dev, table_rows(m), m->tokens, m->pos,
-                                             m->dim, m->x, rope_args(m), m->stream),
+                                             m->dim, m->x, m->stream),
                        "embedding_row");
     }
     for (int pos = pos0; pos < total && !rc; pos++) {
