@@ -579,14 +579,18 @@ __global__ __launch_bounds__(kPwWaves * 64, 2) void q4k_gemm_pw_kernel(const uin
     float4* lv = reinterpret_cast<float4*>(lds + (size_t)wave * kLds);  // [level 2..][tile][q][lane]
     float* dd = reinterpret_cast<float*>(lds + (size_t)wave * kLds + 2 * pw_level_bytes(NT));  // d[32], dmin[32]
 
-    // Workgroup i runs on XCD i % 8: the TP token groups of one 128-row group
-    // get consecutive slots of one XCD, so its weights stream into one L2.
+    // Workgroup i runs on XCD i % 8: consecutive slots of one XCD take its
+    // 128-row groups in turn with the same token group, so the workgroups
+    // running there at once share their token operands in that XCD's L2 (a
+    // row group's weights come back for the next token group from the
+    // memory-side cache).  With 14336 x 4096 at 512 tokens: 100.3 against
+    // 102.0 us per call for row groups as the inner index (four rounds).
     const int id = blockIdx.x, full = (NG / 8) * 8 * TP;
     int rg, tp;
     if (id < full) {
-        const int k = id >> 3;
-        rg = (k / TP) * 8 + (id & 7);
-        tp = k % TP;
+        const int k = id >> 3, NGx = NG / 8;
+        rg = (k % NGx) * 8 + (id & 7);
+        tp = k / NGx;
     } else {
         rg = (NG / 8) * 8 + (id - full) / TP;
         tp = (id - full) % TP;
