@@ -141,8 +141,7 @@ def stream_ceiling(dw, timer, reps):
     """A plain device-to-device copy (torch copy_) of the rotated weight
     copies into one destination, read + write bytes counted: the HBM rate of
     the simplest library kernel on buffers of this size, launch floor
-    included (BASELINE.md asks for a measured stream peak beside the
-    published one)."""
+    included: a measured stream peak beside the published one."""
     import torch
 
     flat = [w for copies in dw for w in copies]

@@ -1,7 +1,7 @@
-"""INTEGRATION.md's error-text lists match the library sources (CPU only).
+"""The integration guide's error-text lists match the library sources (CPU only).
 
 A Rust binding maps libvtq's VTQ_E_INTERNAL text back onto the reference's
-&'static str through the closed list in INTEGRATION.md; a text the library
+&'static str through the closed list in the integration guide; a text the library
 can return but the list lacks would surface as "vtq: internal error".  So
 every string literal passed with VTQ_E_INTERNAL in vtq_api.hip must be in
 the list, and the list must hold nothing else."""
@@ -27,7 +27,7 @@ def library_internal_texts():
 def documented_internal_texts():
     doc = _read("INTEGRATION.md")
     block = re.search(r"const INTERNAL_TEXTS: &\[&str\] = &\[(.*?)\];", doc, re.S)
-    assert block, "INTERNAL_TEXTS list missing from INTEGRATION.md"
+    assert block, "INTERNAL_TEXTS list missing from the integration guide"
     return re.findall(r'"([^"]*)"', block.group(1))
 
 
@@ -53,7 +53,7 @@ def test_reference_texts_are_verbatim():
 
 def test_runtime_texts_are_documented():
     """Every error text of the GGUF parser and the decode driver appears in
-    INTEGRATION.md's status table (with {a,b} alternatives expanded)."""
+    the integration guide's status table (with {a,b} alternatives expanded)."""
     doc = _read("INTEGRATION.md")
     table = doc[doc.index("| status | `Error` variant |"):]
     table = table[:table.index("All of these checks")]
