@@ -133,6 +133,38 @@ SK_SHAPES = [(37, 12 * 256, 70), (33, 22 * 256, 2048), (32, 40 * 256, 100), (64,
              (41, 97 * 256, 31), (100, 64 * 256, 64), (128, 22 * 256, 2048), (130, 43 * 256, 1000)]
 
 
+def _gemm_form(R, N, M):
+    """The form q4k_gemm.hip's gemm_form picks (used to spread the random
+    cases below over all three; the check itself is bit-exactness)."""
+    if N * R * 144 >= 1 << 31:
+        return "lds"
+    if R <= 16:
+        return "sk" if (N + 31) // 32 * ((M + 31) // 32) <= 1024 else "pw2"
+    return "sk" if (N + 31) // 32 * ((M + 127) // 128) < 256 else "lds"
+
+
+def random_gemm_cases(per_form=7, seed=7):
+    rng = np.random.default_rng(seed)
+    got = {"sk": [], "pw2": [], "lds": []}
+    while any(len(v) < per_form for v in got.values()):
+        R = int(rng.choice([1, 2, 3, 5, 8, 11, 16, 17, 22, 33, 43, 64, 100, 127]))
+        M, N = int(rng.integers(32, 641)), int(rng.integers(1, 16385))
+        if M * R * 256 * N > 3e9:
+            continue
+        f = _gemm_form(R, N, M)
+        if len(got[f]) < per_form:
+            got[f].append(pytest.param(M, R * 256, N, id=f"{f}-{M}x{R * 256}x{N}"))
+    return [c for v in got.values() for c in v]
+
+
+# seeded random shapes, seven per GEMM form, up to 3 G multiply-adds each
+@pytest.mark.parametrize("batch,in_f,out_f", random_gemm_cases())
+def test_q4k_prefill_gemm_random_forms(ctx, batch, in_f, out_f):
+    w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 5 + out_f)
+    x = synth.activations(batch * in_f, seed=in_f * 41 + batch)
+    check(ctx, vtq.Q4_K, 0, x, w, batch, in_f, out_f)
+
+
 @pytest.mark.parametrize("batch,in_f,out_f", SK_SHAPES)
 def test_q4k_prefill_gemm_split_k_shapes(ctx, batch, in_f, out_f):
     w = synth.weights(vtq.Q4_K, out_f, in_f, seed=in_f * 7 + out_f)
